@@ -1,0 +1,102 @@
+"""ctypes binding of libukv.so (the gfx950 kernels behind the C ABI in include/ukv.h).
+
+The library is loaded from this package directory only. There is no fallback:
+if it is missing or fails to load, ``load()`` raises and the drop-in modules
+report themselves unavailable, the way the reference reports a missing Triton
+(core/page16_native.py:6-13).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libukv.so"
+
+UKV_DTYPE_F16 = 0
+UKV_DTYPE_BF16 = 1
+
+UKV_OK = 0
+UKV_ERR_INVALID_ARGUMENT = -1
+UKV_ERR_EMPTY = -2
+UKV_ERR_GQA = -3
+UKV_ERR_HEAD_DIM = -4
+UKV_ERR_DTYPE = -5
+UKV_ERR_WORKSPACE = -6
+UKV_ERR_LAUNCH = -7
+UKV_ERR_NO_DEVICE = -8
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); every symbol declared in include/ukv.h.
+SIGNATURES = {
+    "ukv_version": (_c_int, []),
+    "ukv_status_string": (ctypes.c_char_p, [_c_int]),
+    "ukv_page16_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "ukv_page16_decode": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p,  # q, k_cache, v_cache
+            _c_void_p, _c_void_p, _c_void_p,  # block_table, seqlens, out
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # batch, Hq, Hkv, D, n_rep
+            _c_int, _c_int,  # max_blocks, num_pages
+            _c_i64p, _c_i64p, _c_i64p,  # q/k/v strides
+            ctypes.c_float, _c_int,  # softmax_scale, dtype
+            _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libukv.so once and attach the C signatures. Raises on failure."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        _load_error = f"{LIB_PATH} is not built (run __graft_entry__.build())"
+        raise OSError(_load_error)
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    except OSError as exc:
+        _load_error = str(exc)
+        raise
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except OSError:
+        return False
+
+
+def load_error() -> Optional[str]:
+    return _load_error
+
+
+def status_string(code: int) -> str:
+    return load().ukv_status_string(int(code)).decode()
+
+
+def i64_array(values) -> ctypes.Array:
+    vals = [int(v) for v in values]
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def check(code: int, what: str) -> None:
+    if code != UKV_OK:
+        raise RuntimeError(f"{what}: ukv status {code} ({status_string(code)})")
