@@ -117,6 +117,8 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -137,6 +139,17 @@ def main():
         raise RuntimeError("libukv.so is not built/loadable; run __graft_entry__.build() first")
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+
+    if args.calibrate_copy:
+        # A plain device copy of exactly 1 GiB read + 1 GiB written per dispatch.
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 2, "calibrate_copy_bytes_written": dst.numel() * 2,
+                          "dispatches": args.steps}), flush=True)
+        return
 
     layout = workloads.layout_longctx(np.random.default_rng(args.seed))
     log(f"[bench] building config 2 on {torch.cuda.get_device_name(dev)}: B={layout['B']} "

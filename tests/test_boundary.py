@@ -126,3 +126,22 @@ def test_engine_error_classification_substrings():
         with pytest.raises(RuntimeError) as ei:
             _call(*_args(**over))
         assert "shape" in str(ei.value).lower()
+
+
+def test_flat_dropin_import_for_unchanged_scheduler():
+    """core/scheduler.py:14 imports `page16_native` flat; the dropin dir must satisfy it."""
+    import importlib
+    import sys
+
+    dropin = str(ROOT / "unifiedkv_amd" / "dropin")
+    sys.path.insert(0, dropin)
+    try:
+        sys.modules.pop("page16_native", None)
+        mod = importlib.import_module("page16_native")
+        from page16_native import HAS_TRITON as HAS_PAGE16_NATIVE, page16_decode_attention  # noqa: F401
+
+        assert HAS_PAGE16_NATIVE is True
+        assert mod.page16_decode_attention is page16_native.page16_decode_attention
+    finally:
+        sys.path.remove(dropin)
+        sys.modules.pop("page16_native", None)

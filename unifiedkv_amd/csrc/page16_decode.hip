@@ -11,15 +11,15 @@
 //     one wave per KV head, so a workgroup reads each 32 KiB K page and 32 KiB V
 //     page of its chunk whole, and every KV byte is read exactly once for all
 //     n_rep q heads that share it (GQA packing).
-//   * QK^T on the matrix core: one v_mfma_f32_16x16x32 per 32 head dims with
-//     A = the wave's q heads (rows, zero-padded to 16) and B = the page's 16
-//     K rows (columns). K rows are loaded straight from HBM into the B-operand
-//     layout, 16 bytes per lane per step.
-//   * online softmax in log2 units (exp2 with the log2(e) factor folded into
-//     the scale) with 16-lane DPP row reductions.
-//   * P.V in fp32 on the VALU: V rows are loaded 16 bytes per lane with each
-//     row read by D/8 consecutive lanes; p and the rescale factor reach those
-//     lanes through a small per-wave LDS buffer.
+//   * both contractions run on the matrix cores: QK^T with
+//     v_mfma_f32_16x16x32 (K rows as A, q heads as B columns) and P.V with
+//     v_mfma_f32_16x16x16 (the QK result layout is the P operand layout, so P
+//     never leaves the registers). P is split into two 16-bit parts so P.V keeps
+//     fp32-grade weights.
+//   * K and V rows go straight from HBM into registers with 16-byte loads; the
+//     page of step p+1 is in flight while step p is reduced.
+//   * online softmax in log2 units; the running max only moves when a score
+//     exceeds it by more than 2^8, decided by a wave-wide vote.
 //   * a second kernel merges the per-chunk (m, l, acc) partials (log-sum-exp).
 //
 // A reference-faithful scalar kernel (natural exp, one workgroup per (b, h))
@@ -57,26 +57,107 @@ __device__ __forceinline__ int clamp_len(int L, int max_blocks) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
-// Orders LDS traffic of one wave: writes before the barrier are visible to
-// every lane of the wave after it (LDS executes a wave's requests in order).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Splits fp32 softmax weights into two 16-bit parts (p ~= hi + lo, relative
+// error below 2^-16) so that P.V can run on 16-bit MFMA with fp32-grade
+// weights. The fp16 path scales p by 2^7 first so small weights stay normal.
+template <int DT> struct PSplit;
+
+template <> struct PSplit<UKV_DTYPE_BF16> {
+  static constexpr float kScale = 1.f;
+  static __device__ __forceinline__ uint32_t pack(float x0, float x1) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+  }
+  static __device__ __forceinline__ void split(const float (&p)[4], u32x2& hi, u32x2& lo) {
+    hi = u32x2{pack(p[0], p[1]), pack(p[2], p[3])};
+    const float r0 = p[0] - __uint_as_float(hi[0] << 16), r1 = p[1] - __uint_as_float(hi[0] & 0xffff0000u);
+    const float r2 = p[2] - __uint_as_float(hi[1] << 16), r3 = p[3] - __uint_as_float(hi[1] & 0xffff0000u);
+    lo = u32x2{pack(r0, r1), pack(r2, r3)};
+  }
+};
+
+template <> struct PSplit<UKV_DTYPE_F16> {
+  static constexpr float kScale = 128.f;
+  static __device__ __forceinline__ uint32_t pack(float x0, float x1) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+  }
+  static __device__ __forceinline__ void split(const float (&pin)[4], u32x2& hi, u32x2& lo) {
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = pin[r] * kScale;
+    hi = u32x2{pack(p[0], p[1]), pack(p[2], p[3])};
+    const float r0 = p[0] - Elem<UKV_DTYPE_F16>::lo(hi[0]), r1 = p[1] - Elem<UKV_DTYPE_F16>::hi(hi[0]);
+    const float r2 = p[2] - Elem<UKV_DTYPE_F16>::lo(hi[1]), r3 = p[3] - Elem<UKV_DTYPE_F16>::hi(hi[1]);
+    lo = u32x2{pack(r0, r1), pack(r2, r3)};
+  }
+};
+
+#ifndef UKV_PAGE16_PIPE
+#define UKV_PAGE16_PIPE 2
+#endif
+#ifndef UKV_PAGE16_NT
+#define UKV_PAGE16_NT 1
+#endif
+#ifndef UKV_PAGE16_WAVES
+#define UKV_PAGE16_WAVES 8
+#endif
+#ifndef UKV_PAGE16_MIN_WAVES_PER_EU
+#define UKV_PAGE16_MIN_WAVES_PER_EU 1
+#endif
+
+// K/V page rows are read exactly once per call: optionally hint the loads as
+// non-temporal so they do not displace cached lines.
+__device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
+  if constexpr (UKV_PAGE16_NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x2 ld8_stream(const uint16_t* p) {
+  if constexpr (UKV_PAGE16_NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  return *reinterpret_cast<const u32x2*>(p);
 }
 
-template <int DT, int D, int NREP>
-__global__ void __launch_bounds__(512) page16_split_kernel(const DecodeArgs a) {
-  constexpr int STEPS = D / 32;  // MFMA k-steps over the head dimension
-  constexpr int RL = D / 8;      // lanes per V row (8 dims per lane)
-  constexpr int TG = 64 / RL;    // V token groups per wave
-  constexpr int TPL = 16 / TG;   // V tokens per lane per page
-  constexpr int NP = NREP < 4 ? 4 : NREP;
-  constexpr int HG4 = (NREP + 3) / 4;       // QK row groups holding real q heads
-  constexpr int BUF = 16 * NP + NP;         // p[16][NP] followed by alpha[NP]
-  static_assert(TG * TPL == 16, "V layout must cover a page");
+// V row fragment of one lane: DPL = D/16 consecutive dims of one token.
+template <int DPL> struct VRow { uint32_t w[DPL / 2]; };
 
-  __shared__ __attribute__((aligned(16))) float lds_all[8 * 2 * BUF];
+template <int DPL>
+__device__ __forceinline__ void load_vrow(const uint16_t* p, VRow<DPL>& r) {
+  if constexpr (DPL == 4) {
+    const u32x2 x = ld8_stream(p);
+    r.w[0] = x[0];
+    r.w[1] = x[1];
+  } else {
+#pragma unroll
+    for (int c = 0; c < DPL / 8; ++c) {
+      const u32x4 x = ld16_stream(p + 8 * c);
+      r.w[4 * c + 0] = x[0];
+      r.w[4 * c + 1] = x[1];
+      r.w[4 * c + 2] = x[2];
+      r.w[4 * c + 3] = x[3];
+    }
+  }
+}
+
+// Split-K Page16 decode, one wave per KV head, all of that head's q heads
+// (up to 16) per KV read.
+//
+// Lane l = (i16 = l % 16, kg = l / 16).
+//   QK^T  v_mfma_f32_16x16x32: A = the page's K rows (row i16 = token, k-slots
+//         dims 32*s + 8*kg .. +7), B = q^T (column i16 = q head, same dims).
+//         Result: lane l holds S[token 4*kg + r][head i16], r = 0..3.
+//   P.V   v_mfma_f32_16x16x16: A = P (row i16 = head, k = tokens 4*kg .. +3),
+//         which is exactly the QK result layout; B = V (k = tokens 4*kg .. +3,
+//         column i16 -> dim DPL*i16 + e): each lane loads tokens 4*kg .. +3,
+//         dims DPL*i16 .. +DPL-1 and v_perm_b32 regroups the 16-bit elements.
+//         Result tile e: lane l holds O[head 4*kg + r][dim DPL*i16 + e].
+// The running max is only moved when a score exceeds it by more than 2^8
+// (log2 units; weights stay <= 256), decided by a wave-wide vote.
+template <int DT, int D>
+__global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PER_EU) page16_split_kernel(const DecodeArgs a) {
+  constexpr int STEPS = D / 32;  // QK k-steps of 32 dims
+  constexpr int DPL = D / 16;    // V dims per lane = P.V output tiles
+  constexpr float kTau = 8.f;
+  constexpr int kPipe = D > 128 ? 1 : UKV_PAGE16_PIPE;  // D=256 has no registers for a second page
 
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -91,173 +172,206 @@ __global__ void __launch_bounds__(512) page16_split_kernel(const DecodeArgs a) {
   if (p0 >= n_pages) return;
   const int p1 = min(p0 + a.chunk_pages, n_pages);
 
-  float* lds = lds_all + wv * 2 * BUF;
-  const int j = lane & 15;   // QK layout: token column / q row
-  const int kg = lane >> 4;  // QK layout: k-slot group
-  const int rl = lane % RL;  // V layout: dims 8*rl .. 8*rl+7
-  const int tg = lane / RL;  // V layout: tokens tg*TPL .. tg*TPL+TPL-1
-
+  const int i16 = lane & 15;
+  const int kg = lane >> 4;
   const int qh0 = g * a.n_rep;
   const int n_here = min(a.n_rep, a.Hq - qh0);
 
-  // A operand: row j = q head qh0 + j; k-slot group kg at step s covers dims
-  // 32*s + 8*kg .. +7 (the same dims the K rows supply below).
-  u32x4 qa[STEPS];
+  // B operand of QK^T: column i16 = q head qh0 + i16 (zero beyond n_here).
+  u32x4 qb[STEPS];
   {
-    const bool live = j < n_here;
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(qh0 + (live ? j : 0)) * a.q_sh + 8 * kg;
+    const bool live = i16 < n_here;
+    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(qh0 + (live ? i16 : 0)) * a.q_sh + 8 * kg;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) qa[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < STEPS; ++s) qb[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
+  // Page ids of the chunk (at most 128 pages): lane l holds pages p0 + l and
+  // p0 + 64 + l.
   const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
-  const uint16_t* kbase = a.k + (int64_t)j * a.k_st + (int64_t)g * a.k_sh + 8 * kg;
-  const uint16_t* vbase = a.v + (int64_t)(tg * TPL) * a.v_st + (int64_t)g * a.v_sh + 8 * rl;
+  const int bid_lo = (p0 + lane < p1) ? btrow[p0 + lane] : 0;
+  const int bid_hi = (p0 + 64 + lane < p1) ? btrow[p0 + 64 + lane] : 0;
 
-  float m[4], l[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    m[r] = kNegFltMax;
-    l[r] = 0.f;
-  }
-  float acc[NREP][8];
-#pragma unroll
-  for (int h = 0; h < NREP; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  const uint16_t* kbase = a.k + (int64_t)i16 * a.k_st + (int64_t)g * a.k_sh + 8 * kg;
+  const uint16_t* vbase = a.v + (int64_t)(4 * kg) * a.v_st + (int64_t)g * a.v_sh + DPL * i16;
 
-  auto load_page = [&](int p, u32x4 (&kr)[STEPS], u32x4 (&vr)[TPL], int& nv) {
-    int bid = btrow[p];
+  float m_ref = kNegFltMax;  // running max of head i16 (log2 units)
+  float lsum = 0.f;          // this lane's share of that head's sum of weights
+  f32x4 acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto load_page = [&](int p, u32x4 (&kr)[STEPS], VRow<DPL> (&vr)[4], int& nv) {
+    const int idx = p - p0;
+    int bid = __builtin_amdgcn_readlane(idx < 64 ? bid_lo : bid_hi, idx & 63);
     const bool ok = (unsigned)bid < (unsigned)a.num_pages;
     bid = ok ? bid : 0;
     nv = ok ? min(16, L - 16 * p) : 0;
     const uint16_t* kp = kbase + (int64_t)bid * a.k_sp;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) kr[s] = ld16(kp + 32 * s);
+    for (int s = 0; s < STEPS; ++s) kr[s] = ld16_stream(kp + 32 * s);
     const uint16_t* vp = vbase + (int64_t)bid * a.v_sp;
 #pragma unroll
-    for (int i = 0; i < TPL; ++i) vr[i] = ld16(vp + (int64_t)i * a.v_st);
+    for (int t = 0; t < 4; ++t) load_vrow<DPL>(vp + (int64_t)t * a.v_st, vr[t]);
   };
 
-  auto process_page = [&](const u32x4 (&kr)[STEPS], u32x4 (&vr)[TPL], int nv, float* buf) {
+  auto process_page = [&](const u32x4 (&kr)[STEPS], VRow<DPL> (&vr)[4], int nv) {
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) sacc = mfma16x16x32<DT>(qa[s], kr[s], sacc);
-
-    // lane (j, kg) holds the score of q head 4*kg + r against token j.
-    float pr[4], al[4];
+    for (int s = 0; s < STEPS; ++s) sacc = mfma16x16x32<DT>(kr[s], qb[s], sacc);
+    float s2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s2[r] = sacc[r] * a.scale_log2;
+    if (nv < 16) {  // last page of the sequence or an invalid page id
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (4 * kg + r >= nv) {
+          s2[r] = -INFINITY;
+#pragma unroll
+          for (int c = 0; c < DPL / 2; ++c) vr[r].w[c] = 0u;  // junk rows may be non-finite
+        }
+      }
+    }
+    const float mloc = fmaxf(fmaxf(s2[0], s2[1]), fmaxf(s2[2], s2[3]));
+    if (__any(mloc > m_ref + kTau)) {
+      float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
+      mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
+      const float m_new = fmaxf(m_ref, mcol);
+      const float alpha = fast_exp2(m_ref - m_new);
+      lsum *= alpha;
+      m_ref = m_new;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e][r] *= ar;
+      }
+    }
+    float p[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float s2 = (j < nv) ? sacc[r] * a.scale_log2 : -INFINITY;
-      const float mn = fmaxf(m[r], row_max16(s2));
-      al[r] = fast_exp2(m[r] - mn);
-      pr[r] = fast_exp2(s2 - mn);
-      l[r] = l[r] * al[r] + row_sum16(pr[r]);
-      m[r] = mn;
+      p[r] = fast_exp2(s2[r] - m_ref);
+      lsum += p[r];
     }
-    if (kg < HG4) {
-      *reinterpret_cast<f32x4*>(buf + j * NP + 4 * kg) = f32x4{pr[0], pr[1], pr[2], pr[3]};
-      if (j == 0) *reinterpret_cast<f32x4*>(buf + 16 * NP + 4 * kg) = f32x4{al[0], al[1], al[2], al[3]};
+    u32x2 phi, plo;
+    PSplit<DT>::split(p, phi, plo);
+#pragma unroll
+    for (int c = 0; c < DPL / 2; ++c) {
+      const u32x2 blo = {__builtin_amdgcn_perm(vr[1].w[c], vr[0].w[c], 0x05040100u),
+                         __builtin_amdgcn_perm(vr[3].w[c], vr[2].w[c], 0x05040100u)};
+      const u32x2 bhi = {__builtin_amdgcn_perm(vr[1].w[c], vr[0].w[c], 0x07060302u),
+                         __builtin_amdgcn_perm(vr[3].w[c], vr[2].w[c], 0x07060302u)};
+      acc[2 * c] = mfma16x16x16<DT>(phi, blo, acc[2 * c]);
+      acc[2 * c] = mfma16x16x16<DT>(plo, blo, acc[2 * c]);
+      acc[2 * c + 1] = mfma16x16x16<DT>(phi, bhi, acc[2 * c + 1]);
+      acc[2 * c + 1] = mfma16x16x16<DT>(plo, bhi, acc[2 * c + 1]);
     }
-    wave_lds_sync();
-
-    float alpha[NREP];
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) alpha[h] = buf[16 * NP + h];
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
-
-#pragma unroll
-    for (int i = 0; i < TPL; ++i) {
-      const int t = tg * TPL + i;
-      u32x4 w = vr[i];
-      if (t >= nv) w = u32x4{0u, 0u, 0u, 0u};  // masked rows may hold non-finite junk
-      float vf[8];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        vf[2 * c] = Elem<DT>::lo(w[c]);
-        vf[2 * c + 1] = Elem<DT>::hi(w[c]);
-      }
-      const float* prow = buf + t * NP;
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const float ph = prow[h];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(ph, vf[e], acc[h][e]);
-      }
-    }
-    wave_lds_sync();
   };
 
-  // Software pipeline: the loads of page p+1 are in flight while page p is
-  // reduced. Two register sets and two LDS buffers alternate.
-  u32x4 kA[STEPS], vA[TPL], kB[STEPS], vB[TPL];
-  int nvA, nvB;
-  load_page(p0, kA, vA, nvA);
-  int p = p0;
-  for (; p + 1 < p1; p += 2) {
-    load_page(p + 1, kB, vB, nvB);
-    process_page(kA, vA, nvA, lds);
-    if (p + 2 < p1) load_page(p + 2, kA, vA, nvA);
-    process_page(kB, vB, nvB, lds + BUF);
-  }
-  if (p < p1) process_page(kA, vA, nvA, lds);
-
-  // Sum the V-layout token groups.
+  // Software pipeline over PIPE register sets: while page p is reduced, the
+  // loads of pages p+1 .. p+PIPE-1 are in flight.
+  u32x4 kb[kPipe][STEPS];
+  VRow<DPL> vb[kPipe][4];
+  int nvb[kPipe];
 #pragma unroll
-  for (int o = RL; o < 64; o <<= 1)
+  for (int i = 0; i < kPipe - 1; ++i)
+    if (p0 + i < p1) load_page(p0 + i, kb[i], vb[i], nvb[i]);
+  for (int base = p0; base < p1; base += kPipe) {
 #pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], o);
-
-  const int64_t slot = ((int64_t)b * a.max_chunks + chunk) * a.Hq + qh0;
-  if (tg == 0) {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      if (h < n_here) {
-        f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + (slot + h) * D + 8 * rl);
-        dst[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-        dst[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+    for (int u = 0; u < kPipe; ++u) {
+      const int p = base + u;
+      if (p < p1) {
+        const int nxt = (u + kPipe - 1) % kPipe;  // constant after unrolling
+        if (p + kPipe - 1 < p1) load_page(p + kPipe - 1, kb[nxt], vb[nxt], nvb[nxt]);
+        process_page(kb[u], vb[u], nvb[u]);
       }
     }
   }
-  if (j == 0 && kg < HG4) {
+
+  // Column sums of the weights: head i16 over the four token groups.
+  float lcol = lsum + __shfl_xor(lsum, 16);
+  lcol += __shfl_xor(lcol, 32);
+
+  constexpr float kUnscale = 1.f / PSplit<DT>::kScale;
+  const int64_t slot = ((int64_t)b * a.max_chunks + chunk) * a.Hq + qh0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * kg + r;
-      if (h < n_here) a.part_ml[slot + h] = make_float2(m[r], l[r]);
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * kg + r;
+    if (h < n_here) {
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + (slot + h) * D + DPL * i16);
+#pragma unroll
+      for (int c = 0; c < DPL / 4; ++c)
+        dst[c] = f32x4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]} * kUnscale;
     }
   }
+  if (kg == 0 && i16 < n_here) a.part_ml[slot + i16] = make_float2(m_ref, lcol);
 }
 
-// Merges the chunk partials of one (sequence, q head): log-sum-exp in log2 units.
-template <int DT>
-__global__ void __launch_bounds__(64) page16_combine_kernel(const DecodeArgs a) {
+__device__ __forceinline__ float block_reduce_256(float x, float* red, bool is_max) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float y = __shfl_xor(x, o);
+    x = is_max ? fmaxf(x, y) : x + y;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+  __syncthreads();
+  return r;
+}
+
+// Merges the chunk partials of one (sequence, q head): log-sum-exp in log2
+// units. 256 threads: the chunk weights are computed once into LDS, then
+// thread (cs, dq) sums float4 dims 4*dq.. over chunks cs, cs+CS, ... with
+// coalesced row reads, and the CS partial sums meet in LDS.
+template <int DT, int D>
+__global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a) {
+  constexpr int TD = D / 4;       // threads per partial row (float4 each)
+  constexpr int CS = 256 / TD;    // chunk groups
+  extern __shared__ float w_s[];  // [max_chunks] weights, then [CS][D] sums
+  __shared__ float red[4];
+
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const int tid = threadIdx.x;
   const int L = clamp_len(a.lens[b], a.max_blocks);
   const int n_pages = (L + 15) >> 4;
   const int n_chunks = (n_pages + a.chunk_pages - 1) / a.chunk_pages;
   const int64_t base = (int64_t)b * a.max_chunks * a.Hq + h;
 
-  float M = -INFINITY;
-  for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, a.part_ml[base + (int64_t)c * a.Hq].x);
-  float den = 0.f;
-  for (int c = 0; c < n_chunks; ++c) {
+  float mx = -INFINITY;
+  for (int c = tid; c < n_chunks; c += 256) mx = fmaxf(mx, a.part_ml[base + (int64_t)c * a.Hq].x);
+  const float M = block_reduce_256(mx, red, true);
+  float dsum = 0.f;
+  for (int c = tid; c < n_chunks; c += 256) {
     const float2 ml = a.part_ml[base + (int64_t)c * a.Hq];
-    den += ml.y * exp2f(ml.x - M);
+    const float w = exp2f(ml.x - M);
+    w_s[c] = w;
+    dsum += ml.y * w;
   }
-  uint16_t* orow = a.out + ((int64_t)b * a.Hq + h) * a.D;
-  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+  const float den = block_reduce_256(dsum, red, false);  // also orders the w_s writes
+
+  const int cs = tid / TD;
+  const int dq = tid % TD;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const float* po = a.part_o + base * D + 4 * dq;
+  const int64_t cstride = (int64_t)a.Hq * D;
+#pragma unroll 4
+  for (int c = cs; c < n_chunks; c += CS) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(po + (int64_t)c * cstride);
+    const float w = w_s[c];
+    acc += w * v;
+  }
+  float* sums = w_s + ((a.max_chunks + 3) & ~3);
+  *reinterpret_cast<f32x4*>(sums + cs * D + 4 * dq) = acc;
+  __syncthreads();
+  if (tid < D) {
     float num = 0.f;
-    for (int c = 0; c < n_chunks; ++c) {
-      const int64_t s = base + (int64_t)c * a.Hq;
-      num += exp2f(a.part_ml[s].x - M) * a.part_o[s * a.D + d];
-    }
-    orow[d] = Elem<DT>::from_float(n_chunks > 0 ? num / den : NAN);
+#pragma unroll
+    for (int g = 0; g < CS; ++g) num += sums[g * D + tid];
+    a.out[((int64_t)b * a.Hq + h) * D + tid] = Elem<DT>::from_float(n_chunks > 0 ? num / den : NAN);
   }
 }
 
@@ -319,8 +433,8 @@ __global__ void __launch_bounds__(256) page16_scalar_kernel(const DecodeArgs a) 
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kMinChunkPages = 4;
-constexpr int kMaxChunkPages = 64;
+constexpr int kMinChunkPages = 8;
+constexpr int kMaxChunkPages = 128;  // the split kernel keeps a chunk's page ids in two VGPRs
 
 int device_cu_count() {
   static int cached[64] = {0};
@@ -333,16 +447,17 @@ int device_cu_count() {
   return cus;
 }
 
-// Pages per split-K chunk: about four workgroups per CU over the whole batch,
-// overridable with UKV_PAGE16_CHUNK_PAGES for launch-shape sweeps.
+// Pages per split-K chunk: one workgroup per CU over the whole batch (a single
+// round of equal workgroups measured fastest), overridable with
+// UKV_PAGE16_CHUNK_PAGES for launch-shape sweeps.
 int chunk_pages_for(int batch, int max_blocks) {
   const char* env = std::getenv("UKV_PAGE16_CHUNK_PAGES");
   if (env && *env) {
     const int v = std::atoi(env);
-    if (v > 0) return v;
+    if (v > 0) return std::min(v, kMaxChunkPages);
   }
   const long long total = (long long)batch * (long long)std::max(max_blocks, 1);
-  const long long target = 4LL * device_cu_count();
+  const long long target = device_cu_count();
   long long c = (total + target - 1) / target;
   c = std::max<long long>(kMinChunkPages, std::min<long long>(kMaxChunkPages, c));
   return (int)c;
@@ -368,30 +483,38 @@ WorkspaceLayout workspace_layout(int batch, int hq, int d, int max_blocks) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int DT, int D, int NREP>
+template <int DT, int D>
 void launch_split(const DecodeArgs& a, hipStream_t stream) {
-  const int waves = std::min(8, a.n_groups);
+  const int waves = std::min(UKV_PAGE16_WAVES, a.n_groups);
   const dim3 grid(a.max_chunks, a.B, (a.n_groups + waves - 1) / waves);
-  hipLaunchKernelGGL((page16_split_kernel<DT, D, NREP>), grid, dim3(64 * waves), 0, stream, a);
+  hipLaunchKernelGGL((page16_split_kernel<DT, D>), grid, dim3(64 * waves), 0, stream, a);
 }
 
-template <int DT, int D>
-bool dispatch_nrep(const DecodeArgs& a, hipStream_t stream) {
-  if (a.n_rep <= 1) launch_split<DT, D, 1>(a, stream);
-  else if (a.n_rep <= 2) launch_split<DT, D, 2>(a, stream);
-  else if (a.n_rep <= 4) launch_split<DT, D, 4>(a, stream);
-  else if (a.n_rep <= 8) launch_split<DT, D, 8>(a, stream);
-  else if (a.n_rep <= 16) launch_split<DT, D, 16>(a, stream);
-  else return false;
-  return true;
+template <int DT>
+void launch_combine_dt(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid(a.Hq, a.B);
+  const size_t lds = (size_t)(((a.max_chunks + 3) & ~3) + 256 * 4) * sizeof(float);
+  switch (a.D) {
+    case 64: hipLaunchKernelGGL((page16_combine_kernel<DT, 64>), grid, dim3(256), lds, stream, a); break;
+    case 128: hipLaunchKernelGGL((page16_combine_kernel<DT, 128>), grid, dim3(256), lds, stream, a); break;
+    default: hipLaunchKernelGGL((page16_combine_kernel<DT, 256>), grid, dim3(256), lds, stream, a); break;
+  }
+}
+
+void launch_combine(const DecodeArgs& a, int dtype, hipStream_t stream) {
+  if (dtype == UKV_DTYPE_BF16)
+    launch_combine_dt<UKV_DTYPE_BF16>(a, stream);
+  else
+    launch_combine_dt<UKV_DTYPE_F16>(a, stream);
 }
 
 template <int DT>
 bool dispatch_split(const DecodeArgs& a, hipStream_t stream) {
+  if (a.n_rep > 16) return false;
   switch (a.D) {
-    case 64: return dispatch_nrep<DT, 64>(a, stream);
-    case 128: return dispatch_nrep<DT, 128>(a, stream);
-    case 256: return dispatch_nrep<DT, 256>(a, stream);
+    case 64: launch_split<DT, 64>(a, stream); return true;
+    case 128: launch_split<DT, 128>(a, stream); return true;
+    case 256: launch_split<DT, 256>(a, stream); return true;
     default: return false;
   }
 }
@@ -465,11 +588,7 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
         dtype == UKV_DTYPE_BF16 ? dispatch_split<UKV_DTYPE_BF16>(a, stream) : dispatch_split<UKV_DTYPE_F16>(a, stream);
     if (!launched) return UKV_ERR_LAUNCH;
     if (hipGetLastError() != hipSuccess) return UKV_ERR_LAUNCH;
-    const dim3 grid(num_q_heads, batch);
-    if (dtype == UKV_DTYPE_BF16)
-      hipLaunchKernelGGL(page16_combine_kernel<UKV_DTYPE_BF16>, grid, dim3(64), 0, stream, a);
-    else
-      hipLaunchKernelGGL(page16_combine_kernel<UKV_DTYPE_F16>, grid, dim3(64), 0, stream, a);
+    launch_combine(a, dtype, stream);
   } else {
     const dim3 grid(num_q_heads, batch);
     if (dtype == UKV_DTYPE_BF16)

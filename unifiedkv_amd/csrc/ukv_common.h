@@ -13,9 +13,12 @@
 namespace ukv {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegFltMax = -3.4028234663852886e38f;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -61,6 +64,18 @@ template <> __device__ __forceinline__ f32x4 mfma16x16x32<UKV_DTYPE_BF16>(u32x4 
 template <> __device__ __forceinline__ f32x4 mfma16x16x32<UKV_DTYPE_F16>(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// D(16x16, fp32) += A(16x16) * B(16x16) on packed 16-bit operands (4 per lane).
+template <int DT> __device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c);
+
+template <> __device__ __forceinline__ f32x4 mfma16x16x16<UKV_DTYPE_BF16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mfma16x16x16<UKV_DTYPE_F16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                               0);
 }
 
 // ---------------------------------------------------------------------------
