@@ -10,6 +10,12 @@
  * Reference interfaces replaced (paths relative to the BP-KV repository):
  *   ukv_page16_decode      core/page16_native.py:83-150 page16_decode_attention
  *                          (kernel core/page16_native.py:17-80)
+ *   ukv_kv_scatter_tokens  core/pool.py:127-141 PagedKVPool.write_kv_to_blocks
+ *   ukv_kv_gather_tokens   core/pool.py:154-172 PagedKVPool.read_kv_from_blocks
+ *   ukv_page_copy          core/scheduler.py:702-733 _write_block_indexed_layer_to_pool (page gather),
+ *                          core/offload.py:1236-1262 prune_sequence_window (pool->pool compaction),
+ *                          core/offload.py:163-179, 577-597, 662-680 per-page offload/prefetch copies
+ *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
  */
 #ifndef UKV_H_
 #define UKV_H_
@@ -80,6 +86,52 @@ int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
                       int max_blocks, int num_pages, const int64_t* q_strides,
                       const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
                       int dtype, void* workspace, size_t workspace_bytes, ukv_stream_t stream);
+
+/*
+ * Token rows <-> pages for one layer of the pool (bit-exact copies).
+ *   pool_layer   [num_pages, block_size, num_heads, head_dim], element strides pool_strides[0..2]
+ *                (page, token, head); last dimension contiguous
+ *   dense        [num_heads, n_tokens, head_dim], element strides dense_strides[0..1]
+ *                (head, token); last dimension contiguous (the reference's [H_kv, T, D])
+ *   page_ids     int32 [n_ids] device array; token t lives in page page_ids[t / block_size],
+ *                slot t % block_size
+ * Requires n_tokens <= block_size * n_ids. Page ids outside [0, num_pages) are skipped.
+ * Replace core/pool.py:127-141 (write_kv_to_blocks) and :154-172 (read_kv_from_blocks).
+ */
+int ukv_kv_scatter_tokens(void* pool_layer, const int64_t* pool_strides, const void* dense,
+                          const int64_t* dense_strides, const int32_t* page_ids, int n_ids, int num_pages,
+                          int n_tokens, int block_size, int num_heads, int head_dim, ukv_stream_t stream);
+int ukv_kv_gather_tokens(const void* pool_layer, const int64_t* pool_strides, void* dense,
+                         const int64_t* dense_strides, const int32_t* page_ids, int n_ids, int num_pages,
+                         int n_tokens, int block_size, int num_heads, int head_dim, ukv_stream_t stream);
+
+/*
+ * Whole-page copies across layers, for npools (1 or 2: K and V) pool pairs:
+ *   dst_pools[p][layer, dst_ids[layer*dst_ids_layer_stride + j]] =
+ *       src_pools[p][layer, src_ids[layer*src_ids_layer_stride + j]]      j < n, layer < layers
+ * A pool is [layers, pages, page_elems] with element strides {layer, page} given in
+ * src_strides / dst_strides; a page is page_elems contiguous 16-bit elements (multiple of 8).
+ * An id list stride of 0 shares one list across layers. Ids outside [0, src_pages) /
+ * [0, dst_pages) skip that copy. Destination pages must not be source pages of the same call.
+ * Replaces the per-layer index_select / index_put of core/scheduler.py:702-733, the pool->pool
+ * copy of core/offload.py:1236-1262, and the per-page copies of core/offload.py:577-597, 662-680.
+ */
+int ukv_page_copy(const void* const* src_pools, void* const* dst_pools, int npools, const int64_t* src_strides,
+                  const int64_t* dst_strides, const int32_t* src_ids, int64_t src_ids_layer_stride,
+                  const int32_t* dst_ids, int64_t dst_ids_layer_stride, int n, int layers, int page_elems,
+                  int src_pages, int dst_pages, ukv_stream_t stream);
+
+/*
+ * Decode-step append: for each sequence b with len = old_lens[b], write k_new[b] / v_new[b]
+ * ([num_heads, head_dim] rows, strides new_strides[0..1] = {batch, head}) into page
+ * block_table[b, len / block_size], slot len % block_size of the layer's K / V pool, and, if new_lens is not
+ * NULL, store len + 1. Sequences whose page index is >= max_blocks or whose page id is outside
+ * [0, num_pages) are not written. Replaces core/scheduler.py:401-408.
+ */
+int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides, const int64_t* v_strides,
+                  const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
+                  int max_blocks, const int32_t* old_lens, int32_t* new_lens, int batch, int block_size,
+                  int num_heads, int head_dim, int num_pages, ukv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,109 @@
+"""TEST INFRASTRUCTURE ONLY - CPU restatement of the paged pool's integer and copy semantics.
+
+Only tests/ may import this module. Each function follows the cited lines of BP-KV:
+
+* ``FifoAllocator``        core/pool.py:51-58, 96-125 (free list, allocate first n, free appends)
+* ``write_kv_to_blocks``   core/pool.py:127-141 (page i gets tokens 16i .. min(16i+16, T))
+* ``read_kv_from_blocks``  core/pool.py:154-172
+* ``build_block_table``    core/pool.py:174-189 (zero padded int32 [B, max_len])
+* ``kv_append``            core/scheduler.py:401-408 (token at len -> page bt[b, len//16], slot len%16)
+* ``pool_size``            core/pool.py:36-45 (N_total from free memory)
+
+Caches here are numpy arrays [N, 16, H, D] of one layer (any dtype; the copies are bit-exact).
+"""
+from __future__ import annotations
+
+from typing import List
+
+import numpy as np
+
+
+class FifoAllocator:
+    def __init__(self, n_total: int):
+        self.N_total = n_total
+        self.free_blocks: List[int] = list(range(n_total))
+        self.used_blocks = {}
+        self.N_wm_low = max(1, int(0.15 * n_total))
+        self.N_wm_high = max(2, int(0.40 * n_total))
+
+    @property
+    def n_free(self) -> int:
+        return len(self.free_blocks)
+
+    def allocate_blocks(self, n: int) -> List[int]:
+        if len(self.free_blocks) < n:
+            return []
+        ids = self.free_blocks[:n]
+        self.free_blocks = self.free_blocks[n:]
+        for bid in ids:
+            self.used_blocks[bid] = 1
+        return ids
+
+    def free_blocks_by_ids(self, block_ids):
+        for bid in block_ids:
+            if bid in self.used_blocks:
+                del self.used_blocks[bid]
+            self.free_blocks.append(bid)
+
+    def check_watermark(self, n_required: int) -> str:
+        n = len(self.free_blocks)
+        if n < n_required:
+            return "VRAM_FULL"
+        if n < self.N_wm_high:
+            return "WARNING"
+        return "OK"
+
+
+def pool_size(total_bytes: int, used_bytes: int, gpu_mem_frac: float, num_layers: int, block_size: int,
+              num_kv_heads: int, head_dim: int) -> int:
+    reserve = int(0.10 * total_bytes)
+    available = total_bytes - used_bytes - reserve
+    max_kv_mem = int(available * gpu_mem_frac)
+    bytes_per_block = 2 * num_layers * block_size * num_kv_heads * head_dim * 2
+    return max(1, int(max_kv_mem / bytes_per_block))
+
+
+def write_kv_to_blocks(cache: np.ndarray, block_ids, K: np.ndarray) -> None:
+    """cache [N, 16, H, D] (one layer); K [H, T, D]."""
+    seq_len = K.shape[1]
+    for i, bid in enumerate(block_ids):
+        start = i * 16
+        end = min(start + 16, seq_len)
+        chunk = end - start
+        if chunk > 0:
+            cache[bid, :chunk] = K[:, start:end].transpose(1, 0, 2)
+
+
+def read_kv_from_blocks(cache: np.ndarray, block_ids, seq_len: int) -> np.ndarray:
+    chunks = []
+    for i, bid in enumerate(block_ids):
+        start = i * 16
+        end = min(start + 16, seq_len)
+        chunk = end - start
+        if chunk > 0:
+            chunks.append(cache[bid, :chunk].transpose(1, 0, 2))
+    if not chunks:
+        return np.empty((cache.shape[2], 0, cache.shape[3]), dtype=cache.dtype)
+    return np.concatenate(chunks, axis=1)
+
+
+def build_block_table(seq_block_ids_list) -> np.ndarray:
+    batch = len(seq_block_ids_list)
+    max_blocks = max(len(ids) for ids in seq_block_ids_list)
+    bt = np.zeros((batch, max_blocks), dtype=np.int32)
+    for i, ids in enumerate(seq_block_ids_list):
+        if ids:
+            bt[i, : len(ids)] = np.asarray(ids, dtype=np.int32)
+    return bt
+
+
+def kv_append(k_cache: np.ndarray, v_cache: np.ndarray, block_table: np.ndarray, old_lens: np.ndarray,
+              k_new: np.ndarray, v_new: np.ndarray, block_size: int = 16) -> np.ndarray:
+    """k_new / v_new [B, H, D]; returns attn_lens = old_lens + 1."""
+    B = block_table.shape[0]
+    block_pos = old_lens.astype(np.int64) // block_size
+    tok_pos = old_lens.astype(np.int64) % block_size
+    block_ids = block_table[np.arange(B), block_pos]
+    k_cache[block_ids.astype(np.int64), tok_pos] = k_new
+    v_cache[block_ids.astype(np.int64), tok_pos] = v_new
+    return (old_lens + 1).astype(np.int32)

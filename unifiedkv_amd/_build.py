@@ -21,6 +21,7 @@ ARCH = "gfx950"
 SOURCES = [
     "ukv_runtime.hip",
     "page16_decode.hip",
+    "page_ops.hip",
 ]
 
 # Packed-FP32 VALU instructions are disabled for all device code.

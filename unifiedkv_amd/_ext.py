@@ -49,6 +49,34 @@ SIGNATURES = {
             _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
         ],
     ),
+    "ukv_kv_scatter_tokens": (
+        _c_int,
+        [_c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p],
+    ),
+    "ukv_kv_gather_tokens": (
+        _c_int,
+        [_c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_void_p],
+    ),
+    "ukv_page_copy": (
+        _c_int,
+        [
+            ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p), _c_int,  # src pools, dst pools, npools
+            _c_i64p, _c_i64p,  # src / dst strides {layer, page}
+            _c_void_p, ctypes.c_int64, _c_void_p, ctypes.c_int64,  # src ids, stride, dst ids, stride
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # n, layers, page_elems, src/dst pages, stream
+        ],
+    ),
+    "ukv_kv_append": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_i64p, _c_i64p,  # k/v pool layers, strides
+            _c_void_p, _c_void_p, _c_i64p,  # k_new, v_new, strides
+            _c_void_p, _c_int, _c_void_p, _c_void_p,  # block_table, max_blocks, old_lens, new_lens
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # batch, block_size, heads, head_dim, pages, stream
+        ],
+    ),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -95,6 +123,11 @@ def status_string(code: int) -> str:
 def i64_array(values) -> ctypes.Array:
     vals = [int(v) for v in values]
     return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def ptr_array(values) -> ctypes.Array:
+    vals = [ctypes.c_void_p(int(v)) for v in values]
+    return (ctypes.c_void_p * len(vals))(*vals)
 
 
 def check(code: int, what: str) -> None:
