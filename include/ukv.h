@@ -16,6 +16,7 @@
  *                          core/offload.py:1236-1262 prune_sequence_window (pool->pool compaction),
  *                          core/offload.py:163-179, 577-597, 662-680 per-page offload/prefetch copies
  *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
+ *   ukv_select_topk        core/scheduler.py:613-616, core/compress.py:141-142 block top-k + sort
  */
 #ifndef UKV_H_
 #define UKV_H_
@@ -132,6 +133,18 @@ int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strid
                   const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
                   int max_blocks, const int32_t* old_lens, int32_t* new_lens, int batch, int block_size,
                   int num_heads, int head_dim, int num_pages, ukv_stream_t stream);
+
+/*
+ * Retain-set selection: for each row r, the k_r indices i < n_r with the largest scores
+ * (float32 scores[r * row_stride + i]), ties to the lower index, NaN ranked above every
+ * number, written to out[r * out_stride + 0 .. k_r-1] in ascending order; the remaining
+ * entries up to k_max are set to -1. row_n / row_k are optional int32 [rows] device arrays
+ * (NULL: n_max / k_max for every row); k_r is clamped to [0, min(n_r, k_max)].
+ * Replaces torch.topk + sort of core/scheduler.py:613-616 and core/compress.py:141-142, whose
+ * order of equal scores is unspecified.
+ */
+int ukv_select_topk(const float* scores, int64_t row_stride, const int32_t* row_n, const int32_t* row_k, int rows,
+                    int n_max, int k_max, int32_t* out, int64_t out_stride, ukv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ SOURCES = [
     "ukv_runtime.hip",
     "page16_decode.hip",
     "page_ops.hip",
+    "select.hip",
 ]
 
 # Packed-FP32 VALU instructions are disabled for all device code.

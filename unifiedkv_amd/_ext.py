@@ -77,6 +77,11 @@ SIGNATURES = {
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # batch, block_size, heads, head_dim, pages, stream
         ],
     ),
+    "ukv_select_topk": (
+        _c_int,
+        [_c_void_p, ctypes.c_int64, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p, ctypes.c_int64,
+         _c_void_p],
+    ),
 }
 
 _lib: Optional[ctypes.CDLL] = None
