@@ -1,26 +1,34 @@
 #!/usr/bin/env python3
-"""Page16 decode benchmark on one MI355X.
+"""Page16 hot-path benchmark on one MI355X.
 
-Workload: B=16 sequences at ctx=32768 (2048 pages each), H_q=32, H_kv=8,
-D=128, bf16 K/V pool of 40960 pages with fully fragmented (permuted) block
-tables, q/K/V ~ N(0,1), scale 1/sqrt(128). One step = one Page16 decode call
-(one layer-step) through the drop-in ``page16_decode_attention`` -> libukv.so,
-with every input already resident in HBM.
+Default workload (the BASELINE metric, config 2): B=16 sequences at ctx=32768
+(2048 pages each), H_q=32, H_kv=8, D=128, bf16 K/V pool of 40960 pages with
+fully fragmented (permuted) block tables, q/K/V ~ N(0,1), scale 1/sqrt(128).
+One step = one Page16 decode call (one layer-step) through the drop-in
+``page16_decode_attention`` -> libukv.so, with every input resident in HBM.
 
 Prints ONE JSON line:
   value        achieved HBM GB/s = algorithmic bytes / (measured ms per step)
   ms_per_step  wall time per call from HIP events around the K timed calls
-  roofline     the decode kernel's achieved GB/s against MI355X's 8 TB/s
+  roofline     the decode call's achieved GB/s against MI355X's 8 TB/s, with the
+               HBM traffic measured by rocprofv3 FETCH_SIZE/WRITE_SIZE
   cpu_baseline the reference's Page16 page loop restated in C (oracle/),
                timed on this host's cores on a bounded sample of the workload
 Algorithmic bytes per step: each attended token's K and V once (4096 B per
 token), q, out, block table and lengths = 2,147,876,928 B.
+
+Other BASELINE configs (parity cases, measured on request; one JSON line each):
+  --workload ragged            config 3: B=64 lognormal lengths, interleaved pages
+  --workload tiny              config 1: B=4, L~U[256,2048], fp16
+  --workload compaction        config 5a: 32 layers x 8 seqs x 2048 pages -> 419 kept pages
+  --workload offload           config 5b: evicted pages -> pinned host -> new pages
+  --workload compacted_decode  config 5c: decode B=8 at L=6704 on the compacted tables,
+                               rotating through the 32 layers
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -51,8 +59,31 @@ def pmc_traffic_bytes():
     return None
 
 
-def cpu_baseline(tc, layout, budget_s: float):
-    """Time the C page-loop oracle on the host on the first S sequences (bounded)."""
+def event_time_ms(fn, steps, warmup=0):
+    """(mean ms per call over the region, list of per-call ms) with HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    region = start.elapsed_time(end) / steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return region, [a.elapsed_time(b) for a, b in evs]
+
+
+def cpu_baseline(tc, layout, budget_s: float, seqs=None):
+    """Time the C page-loop oracle on the host on a bounded sample of sequences."""
     import numpy as np
     import torch
 
@@ -65,10 +96,11 @@ def cpu_baseline(tc, layout, budget_s: float):
     lens = layout["seqlens"]
     D, Hq, Hkv = layout["D"], layout["Hq"], layout["Hkv"]
     dt = workloads.DTYPE_CODES[layout["dtype"]]
+    order = list(range(layout["B"])) if seqs is None else list(seqs)
 
-    def host_sample(nseq):
+    def host_sample(sel):
         rows, o, ids = [], 0, []
-        for b in range(nseq):
+        for b in sel:
             n = (int(lens[b]) + 15) // 16
             ids.append(bt[b, :n])
             rows.append(np.arange(o, o + n, dtype=np.int32))
@@ -76,8 +108,8 @@ def cpu_baseline(tc, layout, budget_s: float):
         idx = torch.from_numpy(np.concatenate(ids).astype(np.int64)).to(tc["k_cache"].device)
         k = tc["k_cache"].index_select(0, idx).view(torch.int16).cpu().numpy().view(np.uint16)
         v = tc["v_cache"].index_select(0, idx).view(torch.int16).cpu().numpy().view(np.uint16)
-        q = tc["q"][:nseq].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-        return q, k, v, workloads.tables_from_pages(rows), np.ascontiguousarray(lens[:nseq])
+        q = tc["q"][list(sel)].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        return q, k, v, workloads.tables_from_pages(rows), np.ascontiguousarray(lens[list(sel)])
 
     def run(sample):
         q, k, v, t, l = sample
@@ -85,10 +117,10 @@ def cpu_baseline(tc, layout, budget_s: float):
         oracle.page16_decode_pageloop(q, k, v, t, l, softmax_scale=tc["scale"], n_rep=tc["n_rep"], dtype=dt)
         return time.perf_counter() - t0
 
-    s1 = host_sample(1)
+    s1 = host_sample(order[:1])
     t1 = run(s1)
-    nseq = int(max(1, min(layout["B"], round(2.0 / max(t1, 1e-3)))))
-    sample = s1 if nseq == 1 else host_sample(nseq)
+    nseq = int(max(1, min(len(order), round(2.0 / max(t1, 1e-3)))))
+    sample = s1 if nseq == 1 else host_sample(order[:nseq])
     times = []
     t_start = time.perf_counter()
     while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
@@ -102,11 +134,282 @@ def cpu_baseline(tc, layout, budget_s: float):
         "cores": threads,
         "kind": "port",
         "sample": (f"C restatement of core/page16_native.py:34-80 (fp32 page loop, OpenMP over "
-                   f"(seq, q head)) on the first {nseq} of {layout['B']} config-2 sequences "
-                   f"({int(np.sum(sample[4]))} tokens), median of {len(times)} runs"),
-        "us_per_step_equiv": None,
+                   f"(seq, q head)) on {nseq} of {layout['B']} sequences ({int(np.sum(sample[4]))} tokens), "
+                   f"median of {len(times)} runs"),
         "seconds_per_sample_run": round(med, 4),
     }
+
+
+def decode_record(layout, tc, args, workload, metric, *, with_pmc=False, rotate=None):
+    """Time Page16 decode over `tc` (or over rotating layer views) and build the JSON record."""
+    import numpy as np
+
+    from unifiedkv_amd import page16_native, workloads
+
+    step_bytes = workloads.decode_bytes(layout["seqlens"], layout["B"], layout["Hq"], layout["Hkv"], layout["D"],
+                                        layout["block_table"].shape[1])
+    views = rotate or [(tc["k_cache"], tc["v_cache"])]
+    state = {"i": 0}
+
+    def step():
+        k, v = views[state["i"] % len(views)]
+        state["i"] += 1
+        return page16_native.page16_decode_attention(tc["q"], k, v, tc["block_table"], tc["seqlens"],
+                                                     softmax_scale=tc["scale"], n_rep=tc["n_rep"])
+
+    region_ms, per_ms = event_time_ms(step, args.steps, args.warmup)
+    kern_ms = sum(per_ms) / len(per_ms)
+    log(f"[bench] {workload}: region {region_ms * 1e3:.1f} us/step, per-launch mean {kern_ms * 1e3:.1f} us")
+    gbps = step_bytes / (region_ms * 1e-3) / 1e9
+    kern_gbps = step_bytes / (kern_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline sample")
+        cpu = cpu_baseline(tc, layout, args.cpu_seconds)
+        cpu["us_per_step_equiv"] = round(step_bytes / (cpu["value"] * 1e9) * 1e6, 1)
+    return {
+        "metric": metric,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(region_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": layout["dtype"],
+        "data": "synthetic (seeded N(0,1) q/K/V, random-permutation block tables)",
+        "config": {
+            "workload": workload,
+            "batch": layout["B"], "max_ctx": int(np.max(layout["seqlens"])),
+            "total_tokens": int(np.sum(layout["seqlens"])), "num_q_heads": layout["Hq"],
+            "num_kv_heads": layout["Hkv"], "head_dim": layout["D"], "page_size": 16,
+            "pool_pages": layout["N"], "kv_dtype": layout["dtype"],
+        },
+        "us_per_step": round(region_ms * 1e3, 2),
+        "pct_of_peak_hbm": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
+        "algorithmic_bytes_per_step": step_bytes,
+        "roofline": {
+            "bound": "hbm", "achieved": round(kern_gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(kern_gbps / PEAK_HBM_GBPS, 4), "traffic": pmc_traffic_bytes() if with_pmc else None,
+            "kernel_us": round(kern_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+
+
+def run_decode(args, dev):
+    import numpy as np
+
+    from unifiedkv_amd import workloads
+
+    if args.workload == "decode":
+        layout = workloads.layout_longctx(np.random.default_rng(args.seed))
+        tc = workloads.torch_decode_case(layout, args.seed, device=dev)
+        rec = decode_record(layout, tc, args, "page16_decode_config2_longctx", METRIC, with_pmc=True)
+        rec["tokens_per_s_32_layers"] = round(layout["B"] / (32 * rec["ms_per_step"] * 1e-3), 1)
+        return rec
+    if args.workload == "ragged":
+        layout = workloads.layout_ragged(np.random.default_rng(args.seed))
+        tc = workloads.torch_decode_case(layout, args.seed, device=dev)
+        rec = decode_record(layout, tc, args, "page16_decode_config3_ragged",
+                            "Page16 decode GB/s, config 3 ragged B=64 (lognormal median 2048)")
+        rec["config"]["lognormal_sigma"] = layout["sigma"]
+        return rec
+    layout = workloads.layout_tiny(np.random.default_rng(args.seed))
+    case = workloads.numpy_decode_case(layout, args.seed)
+    tc = workloads.to_torch(case, dev)
+    return decode_record(layout, tc, args, "page16_decode_config1_tiny", "Page16 decode GB/s, config 1 tiny B=4 fp16")
+
+
+# ---------------------------------------------------------------------------------- config 5
+C5 = dict(L=32, B=8, ctx=32768, Hkv=8, D=128, sink=64, obs=128, ratio=0.20)
+
+
+def config5_pool(dev, seed, extra_pages):
+    """32-layer bf16 pool holding 8 sequences x 2048 fragmented pages of N(0,1) K/V."""
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd.compaction import selection_budget_blocks
+    from unifiedkv_amd.pool import PagedKVPool
+
+    per = C5["ctx"] // 16
+    k_blocks, eff, _ = selection_budget_blocks(C5["ctx"], sink_len=C5["sink"], obs_len=C5["obs"],
+                                               retain_ratio=C5["ratio"])
+    n_keep = eff // 16
+    N = C5["B"] * per + C5["B"] * n_keep + extra_pages
+    pool = PagedKVPool(16, C5["L"], C5["Hkv"], C5["D"], torch.bfloat16, num_blocks=N, device=dev)
+    src_ids = pool.allocate_blocks(C5["B"] * per)
+    perm = np.random.default_rng(seed).permutation(src_ids)
+    lists = [perm[b * per:(b + 1) * per].tolist() for b in range(C5["B"])]
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    slab = 1024
+    for layer in range(C5["L"]):
+        for lo in range(0, C5["B"] * per, slab):
+            hi = min(C5["B"] * per, lo + slab)
+            for cache in (pool.k_cache, pool.v_cache):
+                cache[layer, lo:hi] = torch.randn((hi - lo,) + tuple(cache.shape[2:]), generator=g, device=dev,
+                                                  dtype=torch.float32).to(torch.bfloat16)
+    scores = torch.rand((C5["B"] * C5["L"], per - (C5["sink"] + C5["obs"]) // 16), generator=g, device=dev)
+    torch.cuda.synchronize()
+    return pool, lists, scores, k_blocks, eff
+
+
+def run_compaction(args, dev):
+    import torch
+
+    from unifiedkv_amd import compaction
+
+    pool, lists, scores, k_blocks, eff = config5_pool(dev, args.seed, 0)
+    L, B = C5["L"], C5["B"]
+    log(f"[bench] config 5a: pool {pool.N_total} pages x {L} layers, k={k_blocks}, keep {eff // 16} pages/seq")
+
+    def plan_and_compact():
+        sel = compaction.select_blocks(scores, k_blocks)
+        retained = [compaction.retained_pages(C5["ctx"], sel[b * L:(b + 1) * L], sink_len=C5["sink"],
+                                              obs_len=C5["obs"]) for b in range(B)]
+        return sel, retained, compaction.compact(pool, lists, retained, [eff] * B)
+
+    t0 = time.perf_counter()
+    sel, retained, res = plan_and_compact()
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    # the same copy again (idempotent: same sources, same destinations) for kernel timing
+    src = torch.cat([torch.tensor(p, dtype=torch.int32, device=dev)[r.long()] for p, r in zip(lists, retained)], 1)
+    dst = torch.tensor([p for ids in res.page_lists for p in ids], dtype=torch.int32, device=dev)
+    copy_ms, per = event_time_ms(lambda: pool.copy_pages(src, dst), args.steps, 2)
+    sel_ms, _ = event_time_ms(lambda: compaction.select_blocks(scores, k_blocks), args.steps, 2)
+    ok = all(torch.equal(pool.k_cache[l, dst.long()], pool.k_cache[l, src[l].long()]) and
+             torch.equal(pool.v_cache[l, dst.long()], pool.v_cache[l, src[l].long()]) for l in range(L))
+    moved = 2 * L * int(dst.numel()) * pool.B * pool.num_kv_heads * pool.head_dim * 2 * 2  # K+V, read+write
+    kern_ms = sum(per) / len(per)
+    gbps = moved / (copy_ms * 1e-3) / 1e9
+    return {
+        "metric": "Config 5a compaction: retained-page gather GB/s (read+write)",
+        "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
+        "ms_per_step": round(copy_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (N(0,1) K/V, U(0,1) page scores)",
+        "config": {"workload": "compaction_config5a", "layers": L, "batch": B, "ctx": C5["ctx"],
+                   "kept_pages_per_seq": eff // 16, "k_mid_blocks": k_blocks},
+        "bit_exact": bool(ok), "moved_bytes": moved,
+        "select_us": round(sel_ms * 1e3, 2), "first_call_with_planning_ms": round(first_ms, 2),
+        "roofline": {"bound": "hbm", "achieved": round(moved / (kern_ms * 1e-3) / 1e9, 2), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(moved / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                     "traffic": None, "kernel_us": round(kern_ms * 1e3, 2)},
+        "cpu_baseline": None,
+    }
+
+
+def run_offload(args, dev):
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd import compaction
+    from unifiedkv_amd.staging import PageStager
+
+    per = C5["ctx"] // 16
+    pool, lists, scores, k_blocks, eff = config5_pool(dev, args.seed, C5["B"] * (per - 419))
+    L, B = C5["L"], C5["B"]
+    sel = compaction.select_blocks(scores, k_blocks)
+    evicted = []
+    for b in range(B):
+        keep = compaction.retained_pages(C5["ctx"], sel[b * L:(b + 1) * L], sink_len=C5["sink"],
+                                         obs_len=C5["obs"]).cpu().numpy()
+        table = np.asarray(lists[b])
+        rows = [table[np.setdiff1d(np.arange(per), keep[l])] for l in range(L)]
+        evicted.append(np.stack(rows))
+    ev_ids = torch.from_numpy(np.concatenate(evicted, axis=1).astype(np.int32))  # [L, B*1629]
+    n = int(ev_ids.shape[1])
+    new_ids = torch.tensor(pool.allocate_blocks(n), dtype=torch.int32)
+    stager = PageStager(pool, chunk_pages=512)
+    nbytes = 2 * L * n * pool.B * pool.num_kv_heads * pool.head_dim * 2
+    log(f"[bench] config 5b: {n} evicted pages per layer, {nbytes / 1e9:.2f} GB each way")
+    # plain pinned copies of the same size class: the link's measured peak
+    probe = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    probe_h = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    d2h_ms, _ = event_time_ms(lambda: probe_h.copy_(probe, non_blocking=True), 5, 1)
+    h2d_ms, _ = event_time_ms(lambda: probe.copy_(probe_h, non_blocking=True), 5, 1)
+    peak_d2h = (1 << 30) / (d2h_ms * 1e-3) / 1e9
+    peak_h2d = (1 << 30) / (h2d_ms * 1e-3) / 1e9
+    host = stager.offload(ev_ids)  # allocates the pinned buffers
+    host.event.synchronize()
+    results = []
+    for _ in range(max(1, min(args.steps, 3))):
+        a = torch.cuda.Event(enable_timing=True)
+        a.record(stager.stream)
+        host = stager.offload(ev_ids, host)
+        ev = stager.prefetch(host, new_ids)
+        stager.wait(ev)
+        d = torch.cuda.Event(enable_timing=True)
+        d.record(stager.stream)
+        torch.cuda.synchronize()
+        results.append(a.elapsed_time(d))
+    b2 = torch.cuda.Event(enable_timing=True)
+    a2 = torch.cuda.Event(enable_timing=True)
+    a2.record(stager.stream)
+    host = stager.offload(ev_ids, host)
+    b2.record(stager.stream)
+    torch.cuda.synchronize()
+    off_ms = a2.elapsed_time(b2)
+    a3 = torch.cuda.Event(enable_timing=True)
+    a3.record(stager.stream)
+    ev = stager.prefetch(host, new_ids)
+    b3 = torch.cuda.Event(enable_timing=True)
+    b3.record(stager.stream)
+    torch.cuda.synchronize()
+    pre_ms = a3.elapsed_time(b3)
+    ok = all(torch.equal(pool.k_cache[l, new_ids.to(dev).long()], pool.k_cache[l, ev_ids[l].to(dev).long()]) and
+             torch.equal(pool.v_cache[l, new_ids.to(dev).long()], pool.v_cache[l, ev_ids[l].to(dev).long()])
+             for l in range(L))
+    rt = sorted(results)[len(results) // 2]
+    return {
+        "metric": "Config 5b offload+prefetch round trip GB/s (each direction)",
+        "value": round(2 * nbytes / (rt * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": len(results), "warmup": 1, "ms_per_step": round(rt, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "offload_config5b", "layers": L, "batch": B, "evicted_pages_per_layer": n,
+                   "bytes_each_way": nbytes},
+        "bit_exact": bool(ok),
+        "offload_gbps": round(nbytes / (off_ms * 1e-3) / 1e9, 2),
+        "prefetch_gbps": round(nbytes / (pre_ms * 1e-3) / 1e9, 2),
+        "roofline": {"bound": "host link", "achieved": round(nbytes / (off_ms * 1e-3) / 1e9, 2),
+                     "peak": round(peak_d2h, 2), "unit": "GB/s",
+                     "frac": round(nbytes / (off_ms * 1e-3) / 1e9 / peak_d2h, 4), "traffic": None,
+                     "peak_h2d": round(peak_h2d, 2), "frac_h2d": round(nbytes / (pre_ms * 1e-3) / 1e9 / peak_h2d, 4),
+                     "peak_source": "1 GiB pinned hipMemcpyAsync in the same process"},
+        "cpu_baseline": None,
+    }
+
+
+def run_compacted_decode(args, dev):
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd import compaction
+
+    pool, lists, scores, k_blocks, eff = config5_pool(dev, args.seed, 0)
+    L, B = C5["L"], C5["B"]
+    sel = compaction.select_blocks(scores, k_blocks)
+    retained = [compaction.retained_pages(C5["ctx"], sel[b * L:(b + 1) * L], sink_len=C5["sink"], obs_len=C5["obs"])
+                for b in range(B)]
+    res = compaction.compact(pool, lists, retained, [eff] * B)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 7)
+    table = np.asarray(res.block_table.cpu())
+    layout = dict(B=B, Hq=32, Hkv=C5["Hkv"], D=C5["D"], dtype="bf16", N=pool.N_total,
+                  seqlens=np.full(B, eff, dtype=np.int32), block_table=table)
+    tc = dict(q=torch.randn((B, 32, C5["D"]), generator=g, device=dev).to(torch.bfloat16),
+              k_cache=pool.k_cache[0], v_cache=pool.v_cache[0], block_table=res.block_table,
+              seqlens=torch.full((B,), eff, dtype=torch.int32, device=dev), scale=C5["D"] ** -0.5, n_rep=4)
+    views = [(pool.k_cache[l], pool.v_cache[l]) for l in range(L)]
+    rec = decode_record(layout, tc, args, "page16_decode_config5c_compacted",
+                        "Config 5c Page16 decode GB/s on compacted tables (B=8, L=6704, 32 rotating layers)",
+                        rotate=views)
+    rec["config"]["layers_rotated"] = L
+    return rec
 
 
 def main():
@@ -117,20 +420,21 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: --gpus {args.gpus} requested, but this build measures the Page16 decode path on one "
+        print(f"bench.py: --gpus {args.gpus} requested, but this build measures the Page16 hot path on one "
               "GPU only (no sharding or collectives are built); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
 
-    from unifiedkv_amd import page16_native, workloads
+    from unifiedkv_amd import page16_native
 
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -151,89 +455,15 @@ def main():
                           "dispatches": args.steps}), flush=True)
         return
 
-    layout = workloads.layout_longctx(np.random.default_rng(args.seed))
-    log(f"[bench] building config 2 on {torch.cuda.get_device_name(dev)}: B={layout['B']} "
-        f"ctx=32768 pool={layout['N']} pages bf16")
-    tc = workloads.torch_decode_case(layout, args.seed, device=dev)
-    torch.cuda.synchronize()
-    step_bytes = workloads.decode_bytes(layout["seqlens"], layout["B"], layout["Hq"], layout["Hkv"], layout["D"],
-                                        layout["block_table"].shape[1])
-
-    def step():
-        return page16_native.page16_decode_attention(tc["q"], tc["k_cache"], tc["v_cache"], tc["block_table"],
-                                                     tc["seqlens"], softmax_scale=tc["scale"], n_rep=tc["n_rep"])
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done; timing {args.steps} steps")
-
-    # whole timed region
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
-
-    # per-launch durations of the decode call on the stream it runs on
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for a, b in evs:
-        a.record()
-        step()
-        b.record()
-    torch.cuda.synchronize()
-    per_launch_ms = [a.elapsed_time(b) for a, b in evs]
-    kern_ms = sum(per_launch_ms) / len(per_launch_ms)
-    log(f"[bench] region {ms_per_step * 1e3:.1f} us/step, per-launch mean {kern_ms * 1e3:.1f} us, "
-        f"min {min(per_launch_ms) * 1e3:.1f} us")
-
-    gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
-    kern_gbps = step_bytes / (kern_ms * 1e-3) / 1e9
-    traffic = pmc_traffic_bytes()
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("[bench] timing the CPU baseline sample")
-        cpu = cpu_baseline(tc, layout, args.cpu_seconds)
-        cpu["us_per_step_equiv"] = round(step_bytes / (cpu["value"] * 1e9) * 1e6, 1)
-        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
-
-    rec = {
-        "metric": METRIC,
-        "value": round(gbps, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/K/V, random-permutation block tables)",
-        "config": {
-            "workload": "page16_decode_config2_longctx",
-            "batch": layout["B"], "ctx": 32768, "num_q_heads": layout["Hq"], "num_kv_heads": layout["Hkv"],
-            "head_dim": layout["D"], "page_size": 16, "pool_pages": layout["N"], "kv_dtype": "bf16",
-        },
-        "us_per_step": round(ms_per_step * 1e3, 2),
-        "pct_of_peak_hbm": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
-        "tokens_per_s_32_layers": round(layout["B"] / (32 * ms_per_step * 1e-3), 1),
-        "algorithmic_bytes_per_step": step_bytes,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(kern_gbps, 2),
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(kern_gbps / PEAK_HBM_GBPS, 4),
-            "traffic": traffic,
-            "kernel_us": round(kern_ms * 1e3, 2),
-        },
-        "cpu_baseline": cpu,
-    }
+    log(f"[bench] workload {args.workload} on {torch.cuda.get_device_name(dev)}")
+    if args.workload in ("decode", "ragged", "tiny"):
+        rec = run_decode(args, dev)
+    elif args.workload == "compaction":
+        rec = run_compaction(args, dev)
+    elif args.workload == "offload":
+        rec = run_offload(args, dev)
+    else:
+        rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)
 
 

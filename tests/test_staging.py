@@ -82,3 +82,21 @@ def test_decode_after_relabelled_prefetch_is_identical(cuda):
     out1 = page16_decode_attention(q, pool.k_cache[layer], pool.v_cache[layer], bt2, lens,
                                    softmax_scale=128 ** -0.5, n_rep=4)
     assert torch.equal(out0.view(torch.int16), out1.view(torch.int16))
+
+
+def test_per_layer_page_lists_round_trip(cuda):
+    """Config 5b evicts a different page set per layer: [layers, n] id lists."""
+    from unifiedkv_amd.staging import PageStager
+
+    pool = _pool(cuda, N=500, L=3, seed=4)
+    rng = np.random.default_rng(5)
+    src = np.stack([rng.permutation(250)[:70] for _ in range(3)]).astype(np.int32)
+    dst = np.stack([250 + rng.permutation(250)[:70] for _ in range(3)]).astype(np.int32)
+    k0 = [pool.k_cache[l, src[l]].clone() for l in range(3)]
+    v0 = [pool.v_cache[l, src[l]].clone() for l in range(3)]
+    st = PageStager(pool, chunk_pages=32)
+    host = st.offload(torch.from_numpy(src))
+    st.wait(st.prefetch(host, torch.from_numpy(dst)))
+    for l in range(3):
+        assert torch.equal(pool.k_cache[l, dst[l]], k0[l])
+        assert torch.equal(pool.v_cache[l, dst[l]], v0[l])

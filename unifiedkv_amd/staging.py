@@ -54,14 +54,23 @@ class PageStager:
         self.stage_v = torch.empty_like(self.stage_k)
         self._iota = torch.arange(self.chunk, dtype=torch.int32, device=self.dev)
 
-    def _ids(self, page_ids: Sequence[int]) -> torch.Tensor:
-        return torch.tensor(list(page_ids), dtype=torch.int32).pin_memory().to(self.dev, non_blocking=True)
+    def _ids(self, page_ids) -> torch.Tensor:
+        """int32 device ids: [n] shared by all layers, or [layers, n] per layer."""
+        if torch.is_tensor(page_ids):
+            return page_ids.to(device=self.dev, dtype=torch.int32).contiguous()
+        host = torch.tensor(page_ids if not isinstance(page_ids, list) or not page_ids or
+                            not isinstance(page_ids[0], (list, tuple)) else [list(r) for r in page_ids],
+                            dtype=torch.int32)
+        return host.pin_memory().to(self.dev, non_blocking=True)
 
-    def offload(self, page_ids: Sequence[int], host: HostPages = None) -> HostPages:
-        """Copy pages `page_ids` (all layers, K and V) to pinned host memory; asynchronous.
+    def offload(self, page_ids, host: HostPages = None) -> HostPages:
+        """Copy pages (all layers, K and V) to pinned host memory; asynchronous.
 
-        Pass a HostPages from an earlier call of the same size to reuse its pinned buffers."""
-        n = len(page_ids)
+        page_ids: [n] ids shared by every layer, or [layers, n] per-layer ids (the pages a
+        per-layer selection evicted). Pass a HostPages from an earlier call of the same size to
+        reuse its pinned buffers. The pages must not be rewritten before ``host.event``."""
+        n = int(page_ids.shape[-1]) if torch.is_tensor(page_ids) else (
+            len(page_ids[0]) if page_ids and isinstance(page_ids[0], (list, tuple)) else len(page_ids))
         pool = self.pool
         if host is None or host.n_pages != n:
             host = HostPages(n_pages=n)
@@ -76,7 +85,7 @@ class PageStager:
             ids = self._ids(page_ids)
             for i, c0 in enumerate(range(0, n, self.chunk)):
                 c = min(self.chunk, n - c0)
-                page_ops.page_copy([pool.k_cache, pool.v_cache], [self.stage_k, self.stage_v], ids[c0:c0 + c],
+                page_ops.page_copy([pool.k_cache, pool.v_cache], [self.stage_k, self.stage_v], ids[..., c0:c0 + c],
                                    self._iota[:c])
                 host.k_chunks[i].copy_(self.stage_k[:, :c], non_blocking=True)
                 host.v_chunks[i].copy_(self.stage_v[:, :c], non_blocking=True)
@@ -84,9 +93,12 @@ class PageStager:
             host.event.record(self.stream)
         return host
 
-    def prefetch(self, host: HostPages, new_page_ids: Sequence[int]) -> torch.cuda.Event:
-        """Write a HostPages back into pages `new_page_ids` (all layers); asynchronous."""
-        if len(new_page_ids) != host.n_pages:
+    def prefetch(self, host: HostPages, new_page_ids) -> torch.cuda.Event:
+        """Write a HostPages back into pages `new_page_ids` ([n] shared or [layers, n]); asynchronous.
+
+        Wait on the returned event (``wait``) before reading the pages."""
+        ids_probe = self._ids(new_page_ids)
+        if int(ids_probe.shape[-1]) != host.n_pages:
             raise ValueError("prefetch: one new page id per offloaded page")
         pool = self.pool
         cur = torch.cuda.current_stream(self.dev)
@@ -94,13 +106,14 @@ class PageStager:
         with torch.cuda.stream(self.stream):
             if host.event is not None:
                 self.stream.wait_event(host.event)
-            ids = self._ids(new_page_ids)
+            ids = ids_probe
+            ids.record_stream(self.stream)  # made on the compute stream, read on this one
             for i, c0 in enumerate(range(0, host.n_pages, self.chunk)):
                 c = min(self.chunk, host.n_pages - c0)
                 self.stage_k[:, :c].copy_(host.k_chunks[i], non_blocking=True)
                 self.stage_v[:, :c].copy_(host.v_chunks[i], non_blocking=True)
                 page_ops.page_copy([self.stage_k, self.stage_v], [pool.k_cache, pool.v_cache], self._iota[:c],
-                                   ids[c0:c0 + c])
+                                   ids[..., c0:c0 + c])
             ev = torch.cuda.Event()
             ev.record(self.stream)
         return ev
