@@ -6,11 +6,14 @@
 // acc/l rounded to the input dtype.
 //
 // Work decomposition (split-K / flash-decoding):
-//   * grid (chunk, sequence, kv-group block). One workgroup streams
-//     `chunk_pages` consecutive pages of one sequence for up to eight KV heads,
-//     one wave per KV head, so a workgroup reads each 32 KiB K page and 32 KiB V
-//     page of its chunk whole, and every KV byte is read exactly once for all
-//     n_rep q heads that share it (GQA packing).
+//   * grid (G workgroups, 1, kv-group blocks), G = one per CU. The batch's
+//     pages, sequence after sequence, form one list of P pages; workgroup w
+//     streams pages [w*P/G, (w+1)*P/G) - equal work for every workgroup however
+//     ragged the lengths - crossing sequence boundaries as needed and leaving
+//     one (m, l, acc) partial per sequence segment. One wave per KV head (up to
+//     eight per workgroup), so a workgroup reads each 32 KiB K page and V page
+//     whole, and every KV byte is read exactly once for all n_rep q heads that
+//     share it (GQA packing).
 //   * both contractions run on the matrix cores: QK^T with
 //     v_mfma_f32_16x16x32 (K rows as A, q heads as B columns) and P.V with
 //     v_mfma_f32_16x16x16 (the QK result layout is the P operand layout, so P
@@ -20,7 +23,7 @@
 //     page of step p+1 is in flight while step p is reduced.
 //   * online softmax in log2 units; the running max only moves when a score
 //     exceeds it by more than 2^8, decided by a wave-wide vote.
-//   * a second kernel merges the per-chunk (m, l, acc) partials (log-sum-exp).
+//   * a second kernel merges each sequence's (m, l, acc) partials (log-sum-exp).
 //
 // A reference-faithful scalar kernel (natural exp, one workgroup per (b, h))
 // serves shapes the split kernel is not instantiated for (head_dim not in
@@ -41,13 +44,15 @@ struct DecodeArgs {
   const int32_t* bt;
   const int32_t* lens;
   uint16_t* out;
-  float* part_o;    // [B][max_chunks][Hq][D]
-  float2* part_ml;  // [B][max_chunks][Hq]: (running max in log2 units, sum of exp2)
+  float* part_o;     // [slots][Hq][D], slots = grid_wgs + B
+  float2* part_ml;   // [slots][Hq]: (running max in log2 units, sum of exp2)
+  int32_t* seq_start;  // [B] first global page of each sequence (written by workgroup 0)
+  int32_t* seq_pages;  // [B] pages of each sequence
   int64_t q_sb, q_sh;
   int64_t k_sp, k_st, k_sh;
   int64_t v_sp, v_st, v_sh;
   int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
-  int chunk_pages, max_chunks;
+  int grid_wgs;      // G: workgroups sharing the batch's pages
   float scale;       // natural-log units (scalar kernel)
   float scale_log2;  // scale * log2(e) (split kernel)
 };
@@ -55,6 +60,24 @@ struct DecodeArgs {
 __device__ __forceinline__ int clamp_len(int L, int max_blocks) {
   const int cap = max_blocks * 16;
   return L < 0 ? 0 : (L > cap ? cap : L);
+}
+
+__device__ __forceinline__ int pages_of(int len, int max_blocks) { return (clamp_len(len, max_blocks) + 15) >> 4; }
+
+__device__ __forceinline__ int wave_sum_i32(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
 }
 
 // Splits fp32 softmax weights into two 16-bit parts (p ~= hi + lo, relative
@@ -163,47 +186,71 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
   const int wv = threadIdx.x >> 6;
   const int g = blockIdx.z * (blockDim.x >> 6) + wv;
   if (g >= a.n_groups) return;  // whole wave leaves; no workgroup barrier below
-  const int b = blockIdx.y;
-  const int chunk = blockIdx.x;
+  const int w = blockIdx.x;
+  const int G = a.grid_wgs;
+  const bool writer = blockIdx.x == 0 && blockIdx.z == 0 && wv == 0;
 
-  const int L = clamp_len(a.lens[b], a.max_blocks);
-  const int n_pages = (L + 15) >> 4;
-  const int p0 = chunk * a.chunk_pages;
-  if (p0 >= n_pages) return;
-  const int p1 = min(p0 + a.chunk_pages, n_pages);
+  // The batch's pages in sequence order form one list of P pages; workgroup w
+  // takes pages [w*P/G, (w+1)*P/G), crossing sequence boundaries as needed.
+  int P = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) {
+    const int bb = c0 + lane;
+    P += wave_sum_i32(bb < a.B ? pages_of(a.lens[bb], a.max_blocks) : 0);
+  }
+  const int x0 = (int)(((int64_t)w * P) / G);
+  const int x1 = (int)(((int64_t)(w + 1) * P) / G);
+  if (x0 >= x1 && !writer) return;
+
+  // Exclusive prefix sums of pages per sequence; the sequence holding page x0.
+  int b_first = -1, s_first = 0, carry = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) {
+    const int bb = c0 + lane;
+    const int n = bb < a.B ? pages_of(a.lens[bb], a.max_blocks) : 0;
+    const int incl = wave_inclusive_scan_i32(n);
+    const int start = carry + incl - n;
+    if (writer && bb < a.B) {
+      a.seq_start[bb] = start;
+      a.seq_pages[bb] = n;
+    }
+    if (b_first < 0) {
+      const uint64_t hit = __ballot(n > 0 && start + n > x0);
+      if (hit) {
+        const int l = __builtin_ctzll(hit);
+        b_first = c0 + l;
+        s_first = __builtin_amdgcn_readlane(start, l);
+        if (!writer) break;
+      }
+    }
+    carry += __builtin_amdgcn_readlane(incl, 63);
+  }
+  if (x0 >= x1) return;
 
   const int i16 = lane & 15;
   const int kg = lane >> 4;
   const int qh0 = g * a.n_rep;
   const int n_here = min(a.n_rep, a.Hq - qh0);
-
-  // B operand of QK^T: column i16 = q head qh0 + i16 (zero beyond n_here).
-  u32x4 qb[STEPS];
-  {
-    const bool live = i16 < n_here;
-    const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(qh0 + (live ? i16 : 0)) * a.q_sh + 8 * kg;
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) qb[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-  }
-
-  // Page ids of the chunk (at most 128 pages): lane l holds pages p0 + l and
-  // p0 + 64 + l.
-  const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
-  const int bid_lo = (p0 + lane < p1) ? btrow[p0 + lane] : 0;
-  const int bid_hi = (p0 + 64 + lane < p1) ? btrow[p0 + 64 + lane] : 0;
+  const bool live = i16 < n_here;
 
   const uint16_t* kbase = a.k + (int64_t)i16 * a.k_st + (int64_t)g * a.k_sh + 8 * kg;
   const uint16_t* vbase = a.v + (int64_t)(4 * kg) * a.v_st + (int64_t)g * a.v_sh + DPL * i16;
 
-  float m_ref = kNegFltMax;  // running max of head i16 (log2 units)
-  float lsum = 0.f;          // this lane's share of that head's sum of weights
+  // Per-segment state (one sequence's share of this workgroup's pages).
+  int b = b_first;   // current sequence
+  int L = 0;         // its attended tokens
+  int pa = 0;        // first page of the segment (within the sequence)
+  int pb = 0;        // one past the last page
+  const int32_t* btrow = nullptr;
+  int bid_win = 0;   // page ids pa + 64*k + lane of the current 64-page window
+
+  u32x4 qb[STEPS];   // B operand of QK^T: column i16 = q head qh0 + i16 (zero beyond n_here)
+  float m_ref;       // running max of head i16 (log2 units)
+  float lsum;        // this lane's share of that head's sum of weights
   f32x4 acc[DPL];
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto load_page = [&](int p, u32x4 (&kr)[STEPS], VRow<DPL> (&vr)[4], int& nv) {
-    const int idx = p - p0;
-    int bid = __builtin_amdgcn_readlane(idx < 64 ? bid_lo : bid_hi, idx & 63);
+    const int idx = p - pa;
+    if (idx != 0 && (idx & 63) == 0) bid_win = (p + lane < pb) ? btrow[p + lane] : 0;
+    int bid = __builtin_amdgcn_readlane(bid_win, idx & 63);
     const bool ok = (unsigned)bid < (unsigned)a.num_pages;
     bid = ok ? bid : 0;
     nv = ok ? min(16, L - 16 * p) : 0;
@@ -268,43 +315,71 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
     }
   };
 
-  // Software pipeline over PIPE register sets: while page p is reduced, the
-  // loads of pages p+1 .. p+PIPE-1 are in flight.
+  constexpr float kUnscale = 1.f / PSplit<DT>::kScale;
   u32x4 kb[kPipe][STEPS];
   VRow<DPL> vb[kPipe][4];
   int nvb[kPipe];
+  int seg_start = s_first;  // global index of page 0 of sequence b
+  int x = x0;
+  while (true) {
+    const int n_b = pages_of(a.lens[b], a.max_blocks);
+    L = clamp_len(a.lens[b], a.max_blocks);
+    pa = x - seg_start;
+    pb = min(x1, seg_start + n_b) - seg_start;
+    btrow = a.bt + (int64_t)b * a.max_blocks;
+    bid_win = (pa + lane < pb) ? btrow[pa + lane] : 0;
+    {
+      const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(qh0 + (live ? i16 : 0)) * a.q_sh + 8 * kg;
 #pragma unroll
-  for (int i = 0; i < kPipe - 1; ++i)
-    if (p0 + i < p1) load_page(p0 + i, kb[i], vb[i], nvb[i]);
-  for (int base = p0; base < p1; base += kPipe) {
+      for (int s = 0; s < STEPS; ++s) qb[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    }
+    m_ref = kNegFltMax;
+    lsum = 0.f;
 #pragma unroll
-    for (int u = 0; u < kPipe; ++u) {
-      const int p = base + u;
-      if (p < p1) {
-        const int nxt = (u + kPipe - 1) % kPipe;  // constant after unrolling
-        if (p + kPipe - 1 < p1) load_page(p + kPipe - 1, kb[nxt], vb[nxt], nvb[nxt]);
-        process_page(kb[u], vb[u], nvb[u]);
+    for (int e = 0; e < DPL; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Software pipeline over PIPE register sets: while page p is reduced, the
+    // loads of pages p+1 .. p+PIPE-1 are in flight.
+#pragma unroll
+    for (int i = 0; i < kPipe - 1; ++i)
+      if (pa + i < pb) load_page(pa + i, kb[i], vb[i], nvb[i]);
+    for (int base = pa; base < pb; base += kPipe) {
+#pragma unroll
+      for (int u = 0; u < kPipe; ++u) {
+        const int p = base + u;
+        if (p < pb) {
+          const int nxt = (u + kPipe - 1) % kPipe;  // constant after unrolling
+          if (p + kPipe - 1 < pb) load_page(p + kPipe - 1, kb[nxt], vb[nxt], nvb[nxt]);
+          process_page(kb[u], vb[u], nvb[u]);
+        }
       }
     }
-  }
 
-  // Column sums of the weights: head i16 over the four token groups.
-  float lcol = lsum + __shfl_xor(lsum, 16);
-  lcol += __shfl_xor(lcol, 32);
-
-  constexpr float kUnscale = 1.f / PSplit<DT>::kScale;
-  const int64_t slot = ((int64_t)b * a.max_chunks + chunk) * a.Hq + qh0;
+    // Column sums of the weights: head i16 over the four token groups.
+    float lcol = lsum + __shfl_xor(lsum, 16);
+    lcol += __shfl_xor(lcol, 32);
+    // Partial slot w + b is unique: a workgroup's sequences are consecutive and
+    // a sequence's workgroups are consecutive.
+    const int64_t slot = (int64_t)(w + b) * a.Hq + qh0;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = 4 * kg + r;
-    if (h < n_here) {
-      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + (slot + h) * D + DPL * i16);
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * kg + r;
+      if (h < n_here) {
+        f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + (slot + h) * D + DPL * i16);
 #pragma unroll
-      for (int c = 0; c < DPL / 4; ++c)
-        dst[c] = f32x4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]} * kUnscale;
+        for (int c = 0; c < DPL / 4; ++c)
+          dst[c] = f32x4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]} * kUnscale;
+      }
     }
+    if (kg == 0 && live) a.part_ml[slot + i16] = make_float2(m_ref, lcol);
+
+    x = seg_start + pb;
+    if (x >= x1) break;
+    seg_start += n_b;
+    ++b;
+    while (b < a.B && pages_of(a.lens[b], a.max_blocks) == 0) ++b;  // empty sequences hold no page
+    if (b >= a.B) break;  // unreachable while x1 <= P; keeps every read inside the batch
   }
-  if (kg == 0 && i16 < n_here) a.part_ml[slot + i16] = make_float2(m_ref, lcol);
 }
 
 __device__ __forceinline__ float block_reduce_256(float x, float* red, bool is_max) {
@@ -322,24 +397,30 @@ __device__ __forceinline__ float block_reduce_256(float x, float* red, bool is_m
   return r;
 }
 
-// Merges the chunk partials of one (sequence, q head): log-sum-exp in log2
-// units. 256 threads: the chunk weights are computed once into LDS, then
-// thread (cs, dq) sums float4 dims 4*dq.. over chunks cs, cs+CS, ... with
+// Merges the partials of one (sequence, q head): log-sum-exp in log2 units.
+// The sequence's pages [S, S+n) of the batch's P pages were split over
+// workgroups w = floor(((S+1)G - 1)/P) .. floor(((S+n)G - 1)/P), whose partials
+// sit in slots w + b. 256 threads: the weights are computed once into LDS, then
+// thread (cs, dq) sums float4 dims 4*dq.. over partials cs, cs+CS, ... with
 // coalesced row reads, and the CS partial sums meet in LDS.
 template <int DT, int D>
 __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a) {
   constexpr int TD = D / 4;       // threads per partial row (float4 each)
   constexpr int CS = 256 / TD;    // chunk groups
-  extern __shared__ float w_s[];  // [max_chunks] weights, then [CS][D] sums
+  extern __shared__ float w_s[];  // [grid_wgs] weights, then [CS][D] sums
   __shared__ float red[4];
 
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  const int L = clamp_len(a.lens[b], a.max_blocks);
-  const int n_pages = (L + 15) >> 4;
-  const int n_chunks = (n_pages + a.chunk_pages - 1) / a.chunk_pages;
-  const int64_t base = (int64_t)b * a.max_chunks * a.Hq + h;
+  const int n_pages = a.seq_pages[b];
+  const int64_t P = (int64_t)a.seq_start[a.B - 1] + a.seq_pages[a.B - 1];
+  const int64_t S = a.seq_start[b];
+  const int G = a.grid_wgs;
+  const int w_first = n_pages > 0 ? (int)(((S + 1) * G - 1) / P) : 0;
+  const int w_last = n_pages > 0 ? (int)(((S + n_pages) * G - 1) / P) : -1;
+  const int n_chunks = w_last - w_first + 1;
+  const int64_t base = (int64_t)(w_first + b) * a.Hq + h;
 
   float mx = -INFINITY;
   for (int c = tid; c < n_chunks; c += 256) mx = fmaxf(mx, a.part_ml[base + (int64_t)c * a.Hq].x);
@@ -364,7 +445,7 @@ __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a)
     const float w = w_s[c];
     acc += w * v;
   }
-  float* sums = w_s + ((a.max_chunks + 3) & ~3);
+  float* sums = w_s + ((a.grid_wgs + 3) & ~3);
   *reinterpret_cast<f32x4*>(sums + cs * D + 4 * dq) = acc;
   __syncthreads();
   if (tid < D) {
@@ -433,8 +514,7 @@ __global__ void __launch_bounds__(256) page16_scalar_kernel(const DecodeArgs a) 
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kMinChunkPages = 8;
-constexpr int kMaxChunkPages = 128;  // the split kernel keeps a chunk's page ids in two VGPRs
+constexpr int kMinPagesPerWg = 8;  // below this a workgroup's setup outweighs its pages
 
 int device_cu_count() {
   static int cached[64] = {0};
@@ -447,37 +527,38 @@ int device_cu_count() {
   return cus;
 }
 
-// Pages per split-K chunk: one workgroup per CU over the whole batch (a single
-// round of equal workgroups measured fastest), overridable with
-// UKV_PAGE16_CHUNK_PAGES for launch-shape sweeps.
-int chunk_pages_for(int batch, int max_blocks) {
-  const char* env = std::getenv("UKV_PAGE16_CHUNK_PAGES");
+// Workgroups G sharing the batch's pages: one per CU (a single round of equal
+// workgroups measured fastest), fewer when even the largest possible batch
+// (batch * max_blocks pages) gives each fewer than kMinPagesPerWg pages;
+// UKV_PAGE16_WGS overrides it for launch-shape sweeps.
+int split_wgs_for(int batch, int max_blocks) {
+  const char* env = std::getenv("UKV_PAGE16_WGS");
   if (env && *env) {
     const int v = std::atoi(env);
-    if (v > 0) return std::min(v, kMaxChunkPages);
+    if (v > 0) return std::min(v, 65535);
   }
-  const long long total = (long long)batch * (long long)std::max(max_blocks, 1);
-  const long long target = device_cu_count();
-  long long c = (total + target - 1) / target;
-  c = std::max<long long>(kMinChunkPages, std::min<long long>(kMaxChunkPages, c));
-  return (int)c;
+  const long long bound = (long long)batch * (long long)std::max(max_blocks, 1);
+  const long long g = std::min<long long>(device_cu_count(), (bound + kMinPagesPerWg - 1) / kMinPagesPerWg);
+  return (int)std::max<long long>(1, g);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct WorkspaceLayout {
-  size_t part_o_off, part_ml_off, total;
-  int chunk_pages, max_chunks;
+  size_t part_o_off, part_ml_off, seq_off, total;
+  int wgs;
 };
 
+// [slots][Hq][D] fp32 partials, [slots][Hq] (m, l), then the per-sequence page
+// starts and counts; slots = G + batch.
 WorkspaceLayout workspace_layout(int batch, int hq, int d, int max_blocks) {
   WorkspaceLayout w{};
-  w.chunk_pages = chunk_pages_for(batch, max_blocks);
-  w.max_chunks = std::max(1, (std::max(max_blocks, 0) + w.chunk_pages - 1) / w.chunk_pages);
-  const size_t slots = (size_t)batch * w.max_chunks * hq;
+  w.wgs = split_wgs_for(batch, max_blocks);
+  const size_t slots = ((size_t)w.wgs + (size_t)batch) * hq;
   w.part_o_off = 0;
   w.part_ml_off = align256(slots * d * sizeof(float));
-  w.total = w.part_ml_off + align256(slots * sizeof(float2));
+  w.seq_off = w.part_ml_off + align256(slots * sizeof(float2));
+  w.total = w.seq_off + align256(2 * (size_t)batch * sizeof(int32_t));
   return w;
 }
 
@@ -486,14 +567,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 template <int DT, int D>
 void launch_split(const DecodeArgs& a, hipStream_t stream) {
   const int waves = std::min(UKV_PAGE16_WAVES, a.n_groups);
-  const dim3 grid(a.max_chunks, a.B, (a.n_groups + waves - 1) / waves);
+  const dim3 grid(a.grid_wgs, 1, (a.n_groups + waves - 1) / waves);
   hipLaunchKernelGGL((page16_split_kernel<DT, D>), grid, dim3(64 * waves), 0, stream, a);
 }
 
 template <int DT>
 void launch_combine_dt(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.Hq, a.B);
-  const size_t lds = (size_t)(((a.max_chunks + 3) & ~3) + 256 * 4) * sizeof(float);
+  const size_t lds = (size_t)(((a.grid_wgs + 3) & ~3) + 256 * 4) * sizeof(float);
   switch (a.D) {
     case 64: hipLaunchKernelGGL((page16_combine_kernel<DT, 64>), grid, dim3(256), lds, stream, a); break;
     case 128: hipLaunchKernelGGL((page16_combine_kernel<DT, 128>), grid, dim3(256), lds, stream, a); break;
@@ -582,8 +663,9 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
     char* ws = static_cast<char*>(workspace);
     a.part_o = reinterpret_cast<float*>(ws + w.part_o_off);
     a.part_ml = reinterpret_cast<float2*>(ws + w.part_ml_off);
-    a.chunk_pages = w.chunk_pages;
-    a.max_chunks = w.max_chunks;
+    a.seq_start = reinterpret_cast<int32_t*>(ws + w.seq_off);
+    a.seq_pages = a.seq_start + batch;
+    a.grid_wgs = w.wgs;
     const bool launched =
         dtype == UKV_DTYPE_BF16 ? dispatch_split<UKV_DTYPE_BF16>(a, stream) : dispatch_split<UKV_DTYPE_F16>(a, stream);
     if (!launched) return UKV_ERR_LAUNCH;
