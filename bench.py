@@ -24,6 +24,8 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
   --workload offload           config 5b: evicted pages -> pinned host -> new pages
   --workload compacted_decode  config 5c: decode B=8 at L=6704 on the compacted tables,
                                rotating through the 32 layers
+  --workload prefill           config 4: chunked prefill, 4 x (16384 prefix + 2048 chunk),
+                               TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak
 """
 from __future__ import annotations
 
@@ -38,6 +40,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 METRIC = "Page16 decode µs/step + achieved HBM GB/s (%peak), B=16 ctx=32K, 1×MI355X"
 PMC_SUMMARY = ROOT / "profiles" / "page16_decode_longctx_pmc.txt"
 
@@ -412,6 +415,106 @@ def run_compacted_decode(args, dev):
     return rec
 
 
+# ---------------------------------------------------------------------------------- config 4
+C4 = dict(B=4, prefix=16384, chunk=2048, Hq=32, Hkv=8, D=128)
+
+
+def prefill_flops(prefix, chunk, Hq, D):
+    """QK^T + PV multiply-adds x 2 over every (query, visible key) pair of one chunk."""
+    pairs = chunk * prefix + chunk * (chunk + 1) // 2
+    return 4 * Hq * D * pairs
+
+
+def prefill_cpu_baseline(tensors, budget_s):
+    """Time the dense fp32 formulation (numpy BLAS) on a bounded slice of sequence 0's chunk rows."""
+    import numpy as np
+    import torch
+
+    from oracle import prefill_oracle
+
+    P, C, Hq, Hkv, D = C4["prefix"], C4["chunk"], C4["Hq"], C4["Hkv"], C4["D"]
+    per = (P + C) // 16
+    ids = tensors["block_table"][0, :per].long()
+    K = tensors["k_cache"].index_select(0, ids).float().cpu().numpy().reshape(per * 16, Hkv, D)
+    V = tensors["v_cache"].index_select(0, ids).float().cpu().numpy().reshape(per * 16, Hkv, D)
+    q = tensors["q"][:C].float().cpu().numpy()
+
+    def run(n):
+        rows = np.arange(C - n, C)  # the last rows see the most keys
+        t0 = time.perf_counter()
+        prefill_oracle.prefill_rows_f32(q[rows], K, V, P + rows, softmax_scale=D ** -0.5, n_rep=Hq // Hkv)
+        return time.perf_counter() - t0
+
+    n = 16
+    while n < C and run(n) < budget_s / 6:  # BLAS efficiency grows with n: size by doubling
+        n *= 2
+    n = min(n, C)
+    times = [run(n) for _ in range(3)]
+    med = sorted(times)[1]
+    flops = 4 * Hq * D * sum(P + int(r) + 1 for r in range(C - n, C))
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"dense fp32 causal attention (numpy BLAS matmul-softmax-matmul, the reference's eager "
+                       f"formulation) of the last {n} of sequence 0's {C} chunk queries x {Hq} heads over "
+                       f"{P + C} keys, median of 3 runs"),
+            "seconds_per_sample_run": round(med, 4)}
+
+
+def run_prefill(args, dev):
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd import prefill
+
+    B, P, C, Hq, Hkv, D = (C4[k] for k in ("B", "prefix", "chunk", "Hq", "Hkv", "D"))
+    rng = np.random.default_rng(args.seed)
+    per = (P + C) // 16
+    N = B * per + 1024
+    bt = torch.from_numpy(rng.permutation(N)[: B * per].reshape(B, per).astype(np.int32)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    mk = lambda *s: torch.randn(s, generator=g, device=dev).to(torch.bfloat16)
+    t = dict(k_cache=mk(N, 16, Hkv, D), v_cache=mk(N, 16, Hkv, D), q=mk(B * C, Hq, D), k_new=mk(B * C, Hkv, D),
+             v_new=mk(B * C, Hkv, D), block_table=bt,
+             cu=torch.arange(0, B * C + 1, C, dtype=torch.int32, device=dev),
+             lens=torch.full((B,), P + C, dtype=torch.int32, device=dev))
+    scale = D ** -0.5
+
+    def step():
+        return prefill.chunked_prefill(t["q"], t["k_new"], t["v_new"], t["k_cache"], t["v_cache"], bt, t["cu"],
+                                       t["lens"], softmax_scale=scale, n_rep=Hq // Hkv, max_chunk=C)
+
+    def attn():
+        return prefill.paged_prefill_attention(t["q"], t["k_cache"], t["v_cache"], bt, t["cu"], t["lens"],
+                                               softmax_scale=scale, n_rep=Hq // Hkv, max_chunk=C)
+
+    flops = B * prefill_flops(P, C, Hq, D)
+    region_ms, _ = event_time_ms(step, args.steps, args.warmup)
+    _, per_attn = event_time_ms(attn, max(1, args.steps // 2), 2)
+    attn_ms = sum(per_attn) / len(per_attn)
+    log(f"[bench] prefill: step {region_ms * 1e3:.1f} us, attention kernel {attn_ms * 1e3:.1f} us")
+    tflops = flops / (region_ms * 1e-3) / 1e12
+    kern_tflops = flops / (attn_ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU baseline sample")
+        cpu = prefill_cpu_baseline(t, args.cpu_seconds)
+    return {
+        "metric": "Config 4 chunked prefill over the paged pool, attention TFLOP/s (4 x (16384 + 2048 chunk))",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(region_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) q/K/V, random-permutation block tables)",
+        "config": {"workload": "paged_prefill_config4", "batch": B, "prefix": P, "chunk": C, "num_q_heads": Hq,
+                   "num_kv_heads": Hkv, "head_dim": D, "page_size": 16, "pool_pages": N},
+        "chunk_tokens_per_s": round(B * C / (region_ms * 1e-3), 1),
+        "algorithmic_flops_per_step": flops,
+        "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kern_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel_us": round(attn_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -421,7 +524,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode"])
+                    choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -462,6 +565,8 @@ def main():
         rec = run_compaction(args, dev)
     elif args.workload == "offload":
         rec = run_offload(args, dev)
+    elif args.workload == "prefill":
+        rec = run_prefill(args, dev)
     else:
         rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)

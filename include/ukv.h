@@ -17,6 +17,9 @@
  *                          core/offload.py:163-179, 577-597, 662-680 per-page offload/prefetch copies
  *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
  *   ukv_select_topk        core/scheduler.py:613-616, core/compress.py:141-142 block top-k + sort
+ *   ukv_kv_write_varlen    core/pool.py:127-141 for a prefill chunk appended after its prefix
+ *   ukv_paged_prefill      core/engine.py:1826-1854 chunked prefill attention over past KV
+ *                          (HF attention / core/varlen.py:19-42 flash_attn_varlen_func, causal)
  */
 #ifndef UKV_H_
 #define UKV_H_
@@ -145,6 +148,37 @@ int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strid
  */
 int ukv_select_topk(const float* scores, int64_t row_stride, const int32_t* row_n, const int32_t* row_k, int rows,
                     int n_max, int k_max, int32_t* out, int64_t out_stride, ukv_stream_t stream);
+
+/*
+ * Prefill-chunk K/V into pages: for sequence b with chunk rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1
+ * (C_b rows) and kv_lens[b] keys after the chunk, row cu_seqlens_q[b] + i of k_new / v_new
+ * ([total, num_heads, head_dim], strides new_strides = {row, head}) goes to position
+ * P_b + i = kv_lens[b] - C_b + i: page block_table[b, pos / 16], slot pos % 16. Positions outside
+ * [0, 16*max_blocks) and page ids outside [0, num_pages) are skipped.
+ */
+int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides, const int64_t* v_strides,
+                        const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
+                        int max_blocks, const int32_t* cu_seqlens_q, const int32_t* kv_lens, int batch,
+                        int max_chunk, int num_heads, int head_dim, int num_pages, ukv_stream_t stream);
+
+/*
+ * Chunked prefill attention over the paged pool. Query row cu_seqlens_q[b] + i (i < C_b) of
+ * sequence b is at position P_b + i, P_b = kv_lens[b] - C_b, and attends to keys
+ * 0 .. P_b + i of the sequence (causal, bottom-right aligned) read through block_table
+ * ([batch, max_blocks] int32, 16-token pages, keys already written - see ukv_kv_write_varlen);
+ * q head h reads KV head h / n_rep.
+ *   q    [total_q, num_q_heads, head_dim], element strides q_strides = {row, head}
+ *   k/v  [num_pages, 16, num_kv_heads, head_dim], strides {page, token, head}
+ *   out  [total_q, num_q_heads, head_dim] contiguous, q's dtype
+ * fp32 softmax and accumulation; a row with no visible key yields NaN. max_chunk bounds C_b.
+ * Replaces the dense chunked prefill of core/engine.py:1826-1854 (HF attention over the past
+ * KV) and core/varlen.py:19-42 (flash_attn_varlen_func, causal=True).
+ */
+int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                      const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch, int total_q,
+                      int max_chunk, int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks,
+                      int num_pages, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                      float softmax_scale, int dtype, ukv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,198 @@
+"""Chunked prefill over the paged pool (row a9).
+
+CPU: the fp64 prefill oracle is pinned by closed forms - its last chunk query
+equals the Page16 decode closed form over the same keys, a single key returns
+V_0, and perturbing keys after a query's position leaves that query unchanged.
+GPU (marked gpu): the chunk K/V write is bit-exact against the restatement and
+the attention matches the oracle to |err| <= 2e-3 + 1e-2 |ref| (NaN-aligned),
+including BASELINE config 4 at full size on sampled (query, head) pairs.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle, prefill_oracle
+from unifiedkv_amd import workloads
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def make_case(seed, prefix, chunk, Hq=32, Hkv=8, D=128, dtype="bf16", extra_pages=7):
+    """Pages hold prefix + chunk tokens; q/k_new/v_new are the chunk's packed rows."""
+    rng = np.random.default_rng(seed)
+    B = len(prefix)
+    kv = [p + c for p, c in zip(prefix, chunk)]
+    pages = [(L + 15) // 16 for L in kv]
+    N = sum(pages) + extra_pages
+    perm = rng.permutation(N).astype(np.int32)
+    lists, o = [], 0
+    for n in pages:
+        lists.append(perm[o:o + n])
+        o += n
+    bt = workloads.tables_from_pages(lists)
+    rnd = lambda shape: workloads._round_bits(rng.standard_normal(shape, dtype=np.float32), dtype)
+    total = sum(chunk)
+    case = dict(k_cache=rnd((N, 16, Hkv, D)), v_cache=rnd((N, 16, Hkv, D)), q=rnd((total, Hq, D)),
+                k_new=rnd((total, Hkv, D)), v_new=rnd((total, Hkv, D)), block_table=bt,
+                cu=np.concatenate([[0], np.cumsum(chunk)]).astype(np.int32), kv_lens=np.array(kv, dtype=np.int32),
+                dtype=dtype, scale=1.0 / math.sqrt(D), n_rep=Hq // Hkv, chunk=list(chunk))
+    return case
+
+
+def written_pool(case):
+    """The pool after the chunk write (bit patterns), by the restatement."""
+    k, v = case["k_cache"].copy(), case["v_cache"].copy()
+    for b in range(len(case["kv_lens"])):
+        rows = slice(case["cu"][b], case["cu"][b + 1])
+        start = int(case["kv_lens"][b]) - (case["cu"][b + 1] - case["cu"][b])
+        prefill_oracle.write_chunk(k, case["block_table"][b], start, case["k_new"][rows])
+        prefill_oracle.write_chunk(v, case["block_table"][b], start, case["v_new"][rows])
+    return k, v
+
+
+def expected(case, rows=None, n_rep=None):
+    dt = workloads.DTYPE_CODES[case["dtype"]]
+    k, v = written_pool(case)
+    f = lambda a: oracle.bits_to_f32(a, dt)
+    return prefill_oracle.prefill_dense(f(case["q"]), f(k), f(v), case["block_table"], case["cu"], case["kv_lens"],
+                                        softmax_scale=case["scale"], n_rep=n_rep or case["n_rep"], rows=rows)
+
+
+# ------------------------------------------------------------------ CPU pinning
+def test_last_chunk_query_equals_decode_closed_form():
+    case = make_case(1, [40, 3], [9, 20], Hq=8, Hkv=2, D=16)
+    out = expected(case)
+    k, v = written_pool(case)
+    f = lambda a: oracle.bits_to_f32(a, oracle.DT_BF16)
+    last_rows = [int(case["cu"][b + 1]) - 1 for b in range(2)]
+    dec = oracle.page16_decode_dense(f(case["q"][last_rows]), f(k), f(v), case["block_table"], case["kv_lens"],
+                                     softmax_scale=case["scale"], n_rep=4)
+    np.testing.assert_allclose(out[last_rows], dec, rtol=1e-12, atol=1e-12)
+
+
+def test_single_key_returns_v0_and_causality():
+    case = make_case(2, [0], [5], Hq=4, Hkv=1, D=16)
+    out = expected(case)
+    f = lambda a: oracle.bits_to_f32(a, oracle.DT_BF16)
+    np.testing.assert_array_equal(out[0], np.broadcast_to(f(case["v_new"][0, 0]), (4, 16)))
+    # keys after a query's position must not matter: change the last chunk row's K/V
+    mod = dict(case)
+    mod["k_new"] = case["k_new"].copy()
+    mod["v_new"] = case["v_new"].copy()
+    mod["k_new"][4] ^= 0x1234
+    mod["v_new"][4] ^= 0x0F0F
+    out2 = expected(mod)
+    np.testing.assert_array_equal(out[:4], out2[:4])
+    assert not np.allclose(out[4], out2[4])
+
+
+# ---------------------------------------------------------------------- GPU
+def to_dev(case, cuda):
+    import torch
+
+    tdt = torch.bfloat16 if case["dtype"] == "bf16" else torch.float16
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(cuda).view(tdt)
+    return dict(q=up(case["q"]), k_new=up(case["k_new"]), v_new=up(case["v_new"]), k_cache=up(case["k_cache"]),
+                v_cache=up(case["v_cache"]), block_table=torch.from_numpy(case["block_table"]).to(cuda),
+                cu=torch.from_numpy(case["cu"]).to(cuda), kv_lens=torch.from_numpy(case["kv_lens"]).to(cuda))
+
+
+def run_gpu(case, cuda, n_rep=None):
+    from unifiedkv_amd import prefill
+
+    t = to_dev(case, cuda)
+    out = prefill.chunked_prefill(t["q"], t["k_new"], t["v_new"], t["k_cache"], t["v_cache"], t["block_table"],
+                                  t["cu"], t["kv_lens"], softmax_scale=case["scale"], n_rep=n_rep or case["n_rep"],
+                                  max_chunk=max(case["chunk"]))
+    return out, t
+
+
+def check(actual, exp, what):
+    ok, err, exc = oracle.allclose_report(actual, exp, ATOL, RTOL)
+    assert ok, f"{what}: max_abs_err={err:.3e} excess={exc:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prefix,chunk", [([0], [37]), ([100, 16], [64, 16]), ([333, 0, 48], [5, 70, 1]),
+                                          ([2000], [300]), ([17], [129])])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_prefill_matches_oracle(cuda, prefix, chunk, dtype):
+    case = make_case(sum(prefix) + sum(chunk), prefix, chunk, dtype=dtype)
+    out, t = run_gpu(case, cuda)
+    import torch
+
+    k_dev = t["k_cache"].view(torch.int16).cpu().numpy().view(np.uint16)
+    k_exp, _ = written_pool(case)
+    np.testing.assert_array_equal(k_dev, k_exp)  # the chunk write, bit-exact
+    check(out.float().cpu().numpy(), expected(case), f"prefix={prefix} chunk={chunk} {dtype}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 32, 128), (16, 8, 128), (64, 8, 128), (16, 1, 128), (32, 8, 64),
+                                      (24, 8, 128), (32, 8, 96)])
+def test_prefill_head_shapes(cuda, Hq, Hkv, D):
+    case = make_case(Hq + D, [50, 7], [40, 33], Hq=Hq, Hkv=Hkv, D=D)
+    out, _ = run_gpu(case, cuda)
+    check(out.float().cpu().numpy(), expected(case), f"Hq={Hq} Hkv={Hkv} D={D}")
+
+
+@pytest.mark.gpu
+def test_prefill_last_row_matches_page16_decode(cuda):
+    """The last query of a chunk sees exactly the decode step's keys."""
+    import torch
+
+    from unifiedkv_amd.page16_native import page16_decode_attention
+
+    case = make_case(9, [500, 260], [64, 40])
+    out, t = run_gpu(case, cuda)
+    last = (t["cu"][1:] - 1).long()
+    dec = page16_decode_attention(t["q"][last].contiguous(), t["k_cache"], t["v_cache"], t["block_table"],
+                                  t["kv_lens"], softmax_scale=case["scale"], n_rep=4)
+    check(out[last].float().cpu().numpy(), dec.float().cpu().numpy(), "prefill last row vs decode")
+
+
+@pytest.mark.gpu
+def test_config4_full_size_sampled(cuda):
+    """4 sequences x (16384-token prefix + 2048-token chunk), H_q=32, H_kv=8, D=128, bf16."""
+    import torch
+
+    from unifiedkv_amd import prefill
+
+    rng = np.random.default_rng(44)
+    B, P, C, Hq, Hkv, D = 4, 16384, 2048, 32, 8, 128
+    per = (P + C) // 16
+    N = B * per + 1000
+    perm = rng.permutation(N).astype(np.int32)
+    bt = perm[: B * per].reshape(B, per)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(4)
+    mk = lambda *s: torch.randn(s, generator=g, device=cuda).to(torch.bfloat16)
+    k_cache, v_cache = mk(N, 16, Hkv, D), mk(N, 16, Hkv, D)
+    q, k_new, v_new = mk(B * C, Hq, D), mk(B * C, Hkv, D), mk(B * C, Hkv, D)
+    cu = torch.arange(0, B * C + 1, C, dtype=torch.int32, device=cuda)
+    lens = torch.full((B,), P + C, dtype=torch.int32, device=cuda)
+    btd = torch.from_numpy(bt).to(cuda)
+    out = prefill.chunked_prefill(q, k_new, v_new, k_cache, v_cache, btd, cu, lens, softmax_scale=D ** -0.5,
+                                  n_rep=4, max_chunk=C)
+    torch.cuda.synchronize()
+    samples = [(int(b * C + i), int(h)) for b, i, h in zip(rng.integers(0, B, 24), rng.integers(0, C, 24),
+                                                          rng.integers(0, Hq, 24))]
+    samples += [(0, 0), (C - 1, 31), (B * C - 1, 5), (2 * C, 17)]
+    # host copies of only the pages the sampled sequences use
+    seqs = sorted({r // C for r, _ in samples})
+    ids = torch.from_numpy(bt[seqs].reshape(-1).astype(np.int64)).to(cuda)
+    kk = k_cache.index_select(0, ids).float().cpu().numpy()
+    vv = v_cache.index_select(0, ids).float().cpu().numpy()
+    sub_bt = np.arange(len(seqs) * per, dtype=np.int32).reshape(len(seqs), per)
+    qf = q.float().cpu().numpy()
+    rows = []
+    for r, h in samples:
+        s = seqs.index(r // C)
+        rows.append((s * C + r % C, h))
+    sub_q = np.concatenate([qf[b * C:(b + 1) * C] for b in seqs])
+    exp = prefill_oracle.prefill_dense(sub_q, kk, vv, sub_bt, np.arange(0, len(seqs) * C + 1, C),
+                                       np.full(len(seqs), P + C), softmax_scale=D ** -0.5, n_rep=4, rows=rows)
+    got = out.float().cpu().numpy()
+    for (r, h), (rr, hh) in zip(samples, rows):
+        check(got[r, h], exp[(rr, hh)], f"config4 row {r} head {h}")

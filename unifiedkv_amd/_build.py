@@ -23,6 +23,7 @@ SOURCES = [
     "page16_decode.hip",
     "page_ops.hip",
     "select.hip",
+    "paged_prefill.hip",
 ]
 
 # Packed-FP32 VALU instructions are disabled for all device code.

@@ -77,6 +77,23 @@ SIGNATURES = {
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # batch, block_size, heads, head_dim, pages, stream
         ],
     ),
+    "ukv_kv_write_varlen": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_i64p, _c_i64p, _c_void_p, _c_void_p, _c_i64p,  # pools, strides, k/v new
+            _c_void_p, _c_int, _c_void_p, _c_void_p,  # block_table, max_blocks, cu_seqlens_q, kv_lens
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # batch, max_chunk, heads, head_dim, pages, stream
+        ],
+    ),
+    "ukv_paged_prefill": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q k v bt cu kv_lens out
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,  # batch total_q max_chunk Hq Hkv D n_rep
+            _c_int, _c_int, _c_i64p, _c_i64p, _c_i64p,  # max_blocks num_pages strides
+            ctypes.c_float, _c_int, _c_void_p,  # scale dtype stream
+        ],
+    ),
     "ukv_select_topk": (
         _c_int,
         [_c_void_p, ctypes.c_int64, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p, ctypes.c_int64,
