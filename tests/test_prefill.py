@@ -138,6 +138,22 @@ def test_prefill_head_shapes(cuda, Hq, Hkv, D):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("big", [70000.0, 3.0e38])
+def test_prefill_bf16_v_beyond_fp16_range(cuda, big):
+    """bf16 V values that fp16 cannot hold take the fp32 fallback and still match."""
+    case = make_case(77, [300, 40], [64, 25])
+    bits = workloads._round_bits(np.array([big, -big / 3], dtype=np.float32), "bf16")
+    case["v_cache"][case["block_table"][0][3], 5, 2, 7] = bits[0]  # a prefix key of sequence 0
+    case["v_new"][70, 1, 100] = bits[1]  # a chunk key of sequence 1
+    out, _ = run_gpu(case, cuda)
+    got = out.float().cpu().numpy()
+    exp = expected(case)
+    fin = np.isfinite(exp)
+    assert np.array_equal(np.isfinite(got), fin)
+    check(np.where(fin, got, 0.0), np.where(fin, exp, 0.0), f"bf16 V with |v| = {big}")
+
+
+@pytest.mark.gpu
 def test_prefill_last_row_matches_page16_decode(cuda):
     """The last query of a chunk sees exactly the decode step's keys."""
     import torch

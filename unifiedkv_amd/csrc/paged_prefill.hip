@@ -11,23 +11,31 @@
 // are read from 16-token pages through the block table, and
 // ukv_kv_write_varlen first writes the chunk's own K/V into its pages.
 //
-// Kernel: grid (query blocks, KV groups, sequences), 4 waves. A workgroup takes
-// QW = 4 * CB * (16 / n_rep) consecutive queries of one KV group. Within a
+// Kernel: one workgroup of W waves (W = 8 by default, two per SIMD) takes
+// QW = W * 2 * (16 / n_rep) consecutive queries of one KV group. Within a
 // wave, an MFMA column is a (query, q head) pair: 16 / n_rep queries times the
-// n_rep q heads of the group, so one K/V read serves the whole GQA group.
-//   * key tiles of 32 keys (two pages) are staged in LDS (double buffered, rows
-//     padded to 272 B so 16 lanes reading 16 rows hit distinct banks) and
-//     shared by the 4 waves;
-//   * S^T = K Q^T on v_mfma_f32_16x16x32 (A = 16 keys x 32 dims from LDS,
-//     B = the wave's q columns held in registers); lane l ends with keys
-//     4*(l/16) + r of column l % 16;
-//   * online softmax per column in log2 units, causal and validity masks, and
-//     the running max moved only when a score exceeds it by 2^8 (wave vote);
-//   * P.V on v_mfma_f32_16x16x32 (bf16 P as a rounded value plus its
-//     residual, two MFMAs; fp16 P rounded once): the S^T layout is
-//     already P's A-operand layout (k-slots = the lane's 8 keys of the tile);
-//     V's B operands come from 8 LDS row reads per lane regrouped with
-//     v_perm_b32.
+// n_rep q heads of the group, so one K/V read serves the whole GQA group; a
+// wave holds two 16-column blocks.
+//   * workgroups are ordered so that each XCD (dispatch is round-robin over the
+//     8 XCDs) runs consecutive work items: the query blocks of one (sequence,
+//     group) share that XCD's L2 while they stream the same pages;
+//   * key tiles of 32 keys (two pages) pass through registers into a 3-stage
+//     LDS ring (rows padded to 272 B), one barrier per tile; the loads of tile
+//     t+2 are in flight while tile t is computed;
+//   * S^T = K Q^T on v_mfma_f32_16x16x32 in the input type (A = 16 keys x 32
+//     dims from LDS, B = the wave's q columns in registers); lane l ends with
+//     keys 4*(l/16) + r of column l % 16;
+//   * online softmax per column in log2 units; masks only on tiles that touch
+//     the sequence end, an invalid page or the causal diagonal; the running max
+//     moves only when a score exceeds it by 2^8 (wave vote);
+//   * P.V on v_mfma_f32_16x16x32_f16: P is rounded to fp16 (11 significant
+//     bits, 4x finer than a bf16 P) and, for bf16 pools, the loader converts
+//     the V tile to fp16, which is exact for |v| < 65520 (a tile holding a
+//     larger or infinite value stays bf16 and takes P as a bf16 value plus its
+//     bf16 residual on two MFMAs). The S^T layout is already P's A-operand
+//     layout; V's B operands come from 8 LDS row reads per lane regrouped
+//     with v_perm_b32; the softmax denominators come from one more MFMA
+//     against a ones operand, so they sum exactly the rounded P.
 #include <algorithm>
 #include <cmath>
 
@@ -46,7 +54,7 @@ struct PrefillArgs {
   const int32_t* bt;
   const int32_t* cu_q;     // [B+1]
   const int32_t* kv_lens;  // [B] keys per sequence, the chunk included
-  int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
+  int B, Hq, n_rep, n_groups, D, max_blocks, num_pages, n_qblocks;
   float scale, scale_log2;
 };
 
@@ -56,123 +64,245 @@ __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
-template <int DT> __device__ __forceinline__ uint32_t pack2(float x0, float x1);
-template <> __device__ __forceinline__ uint32_t pack2<UKV_DTYPE_BF16>(float x0, float x1) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
-}
-template <> __device__ __forceinline__ uint32_t pack2<UKV_DTYPE_F16>(float x0, float x1) {
+__device__ __forceinline__ uint32_t pack_f16(float x0, float x1) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, f16x2));
 }
+__device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+}
 
-#ifndef UKV_PREFILL_SPLIT_P
-#define UKV_PREFILL_SPLIT_P 1
+// Two bf16 values -> two fp16 values (RNE; exact when 2^-14 <= |x| < 65520),
+// folding |x| into amax.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float& amax) {
+  const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xffff0000u);
+  amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+  return pack_f16(lo, hi);
+}
+
+#ifndef UKV_PREFILL_WAVES
+#define UKV_PREFILL_WAVES 8
 #endif
 
 constexpr int kTileKeys = 32;
 constexpr int kRowPad = 136;  // LDS row pitch in 16-bit elements (128 + 8)
+constexpr int kStages = 3;
+constexpr int kColBlocks = 2;  // 16-column blocks per wave
+constexpr float kF16Limit = 65504.f;
 
-template <int DT, int CB>
-__global__ void __launch_bounds__(256) paged_prefill_kernel(const PrefillArgs a) {
+// Fallback for a workgroup whose key range holds a bf16 V value of magnitude
+// >= 65520 (or infinite), which fp16 cannot carry: every (query, head) pair
+// of the workgroup is recomputed in fp32 on the vector ALUs, one pair per
+// wave at a time, keys in page order (the reference's order), natural exp.
+// D = 128: lane l owns dims 2l and 2l + 1.
+template <int DT>
+__device__ void prefill_pairs_fp32(const PrefillArgs& a, int b, int g, int q_begin, int C, int P0, int Lk, int qa,
+                                   int qe, int wv, int nwaves, int lane) {
+  const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
+  const int npairs = (qe - qa) * a.n_rep;
+  for (int pi = wv; pi < npairs; pi += nwaves) {
+    const int qi = qa + pi / a.n_rep;
+    const int h = g * a.n_rep + pi % a.n_rep;
+    if (qi >= C || h >= a.Hq) continue;
+    const int L = max(0, min(Lk, P0 + qi + 1));
+    const uint16_t* qrow = a.q + (int64_t)(q_begin + qi) * a.q_st + (int64_t)h * a.q_sh + 2 * lane;
+    const float q0 = Elem<DT>::one(qrow[0]), q1 = Elem<DT>::one(qrow[1]);
+    float m = kNegFltMax, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+    for (int key = 0; key < L; ++key) {
+      const int id = btrow[key >> 4];
+      if ((unsigned)id >= (unsigned)a.num_pages) continue;
+      const uint16_t* kr = a.k + (int64_t)id * a.k_sp + (int64_t)(key & 15) * a.k_st + (int64_t)g * a.k_sh + 2 * lane;
+      const uint16_t* vr = a.v + (int64_t)id * a.v_sp + (int64_t)(key & 15) * a.v_st + (int64_t)g * a.v_sh + 2 * lane;
+      float part = q0 * Elem<DT>::one(kr[0]) + q1 * Elem<DT>::one(kr[1]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+      const float sc = part * a.scale;
+      const float mn = fmaxf(m, sc);
+      const float alpha = expf(m - mn), pk = expf(sc - mn);
+      l = l * alpha + pk;
+      acc0 = acc0 * alpha + pk * Elem<DT>::one(vr[0]);
+      acc1 = acc1 * alpha + pk * Elem<DT>::one(vr[1]);
+      m = mn;
+    }
+    uint16_t* orow = a.out + ((int64_t)(q_begin + qi) * a.Hq + h) * 128 + 2 * lane;
+    orow[0] = Elem<DT>::from_float(acc0 / l);
+    orow[1] = Elem<DT>::from_float(acc1 / l);
+  }
+}
+
+template <int DT, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+paged_prefill_kernel(const PrefillArgs a) {
   constexpr int D = 128;
   constexpr int STEPS = D / 32;
+  constexpr int NT = 64 * WAVES;
+  constexpr int ITEMS = kTileKeys * 16 / NT;  // 16-byte chunks per thread per tensor per tile
+  constexpr int CB = kColBlocks;
   constexpr float kTau = 8.f;
-  constexpr bool kSplitP = DT == UKV_DTYPE_BF16 && UKV_PREFILL_SPLIT_P;
-  __shared__ __attribute__((aligned(16))) uint16_t k_s[2][kTileKeys][kRowPad];
-  __shared__ __attribute__((aligned(16))) uint16_t v_s[2][kTileKeys][kRowPad];
-  __shared__ int valid_s[2][kTileKeys];
+  constexpr bool kBf16 = DT == UKV_DTYPE_BF16;
+  static_assert(ITEMS * NT == kTileKeys * 16, "loader mapping");
+  __shared__ __attribute__((aligned(16))) uint16_t k_s[kStages][kTileKeys][kRowPad];
+  __shared__ __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kRowPad];  // fp16
+  __shared__ int wide_s[kStages];  // = tile index when that tile's bf16 V holds |v| >= 65520
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int i16 = lane & 15;
   const int kg = lane >> 4;
-  const int g = blockIdx.y;
-  const int b = blockIdx.z;
+
+  // Work item of this workgroup: each XCD takes a contiguous range.
+  const int n_qb = a.n_qblocks;
+  const int total = n_qb * a.n_groups * a.B;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int per = total >> 3, rem = total & 7;
+  const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+  const int qblk = n_qb - 1 - work % n_qb;  // the longest query blocks of a group first
+  const int g = (work / n_qb) % a.n_groups;
+  const int b = work / (n_qb * a.n_groups);
 
   const int qpb = 16 / a.n_rep;  // queries per column block
-  const int qw = 4 * CB * qpb;   // queries per workgroup
+  const int qw = WAVES * CB * qpb;
   const int q_begin = a.cu_q[b];
   const int C = a.cu_q[b + 1] - q_begin;
-  const int q0 = blockIdx.x * qw;
+  const int q0 = qblk * qw;
   if (q0 >= C) return;  // whole workgroup
   const int Lk = kv_len_of(a, b);
   const int P0 = Lk - C;  // keys before the chunk
-  const int q_last = min(C, q0 + qw) - 1;
-  const int kend = max(0, min(Lk, P0 + q_last + 1));
+  const int kend = max(0, min(Lk, P0 + min(C, q0 + qw)));
   const int n_tiles = (kend + kTileKeys - 1) / kTileKeys;
+  const int n_pg = (kend + 15) >> 4;
 
-  // This lane's columns: (query, head) of column i16 in each column block.
-  const int head_local = i16 % a.n_rep;
-  const int head = g * a.n_rep + head_local;
+  // This wave's queries and this lane's columns.
+  const int wq0 = q0 + wv * CB * qpb;
+  const bool wave_live = wq0 < C;
+  const int wpos_min = P0 + wq0;
+  const int head = g * a.n_rep + i16 % a.n_rep;
   int qpos[CB];  // absolute position of the column's query, or -1 if the column is unused
-  u32x4 qb[CB][STEPS];
+  u32x4 qv[CB][STEPS];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const int qi = q0 + (wv * CB + cb) * qpb + i16 / a.n_rep;
+    const int qi = wq0 + cb * qpb + i16 / a.n_rep;
     const bool live = qi < C && head < a.Hq;
     qpos[cb] = live ? P0 + qi : -1;
     const uint16_t* qp = a.q + (int64_t)(q_begin + (live ? qi : 0)) * a.q_st + (int64_t)(live ? head : 0) * a.q_sh +
                          8 * kg;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) qb[cb][s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < STEPS; ++s) qv[cb][s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  float m_ref[CB], lsum[CB];
+  float m_ref[CB];
   f32x4 o[CB][8];
+  f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     m_ref[cb] = kNegFltMax;
-    lsum[cb] = 0.f;
+    lacc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[cb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Tile loader: thread t moves 16-byte chunk t % 16 of rows t / 16 and
-  // 16 + t / 16 of the K and the V tile (rows = keys).
-  const int lrow = tid >> 4;
-  const int lchunk = tid & 15;
+  // ---- tile loader: chunk idx = tid + i * NT is 16-byte chunk idx % 16 of key row idx / 16.
   const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
-  u32x4 ldk[2], ldv[2];
-  int ldok[2];
-  auto fetch_tile = [&](int t) {
+  auto page_id = [&](int pg) -> int { return pg < n_pg ? btrow[pg] : -1; };
+  auto page_ok = [&](int id) -> bool { return (unsigned)id < (unsigned)a.num_pages; };
+  u32x4 rk[ITEMS], rv[ITEMS];
+  auto issue = [&](int u, int id0, int id1) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int key = t * kTileKeys + h * 16 + lrow;
-      int page = key < Lk ? btrow[key >> 4] : -1;
-      const bool ok = (unsigned)page < (unsigned)a.num_pages;
-      ldok[h] = ok;
-      page = ok ? page : 0;
-      const int64_t kt = (int64_t)page * a.k_sp + (int64_t)(key & 15) * a.k_st + (int64_t)g * a.k_sh + 8 * lchunk;
-      const int64_t vt = (int64_t)page * a.v_sp + (int64_t)(key & 15) * a.v_st + (int64_t)g * a.v_sh + 8 * lchunk;
-      ldk[h] = ok ? ld16(a.k + kt) : u32x4{0u, 0u, 0u, 0u};
-      ldv[h] = ok ? ld16(a.v + vt) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = tid + i * NT;
+      const int row = idx >> 4, ch = idx & 15;
+      const int id = row < 16 ? id0 : id1;
+      const int pg = page_ok(id) ? id : 0;
+      const int tok = row & 15;
+      rk[i] = ld16(a.k + (int64_t)pg * a.k_sp + (int64_t)tok * a.k_st + (int64_t)g * a.k_sh + 8 * ch);
+      rv[i] = ld16(a.v + (int64_t)pg * a.v_sp + (int64_t)tok * a.v_st + (int64_t)g * a.v_sh + 8 * ch);
     }
   };
-  auto store_tile = [&](int buf) {
+  // Zero V rows past the sequence or on an invalid page; a bf16 V becomes
+  // fp16, and a magnitude that fp16 cannot hold flags the tile.
+  auto prepare = [&](int u, int id0, int id1) {
+    const bool full = page_ok(id0) && page_ok(id1) && kTileKeys * (u + 1) <= Lk;
+    float amax = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *reinterpret_cast<u32x4*>(&k_s[buf][h * 16 + lrow][8 * lchunk]) = ldk[h];
-      *reinterpret_cast<u32x4*>(&v_s[buf][h * 16 + lrow][8 * lchunk]) = ldv[h];
-      if (lchunk == 0) valid_s[buf][h * 16 + lrow] = ldok[h];
+    for (int i = 0; i < ITEMS; ++i) {
+      const int row = (tid + i * NT) >> 4;
+      if (!full) {
+        const bool ok = page_ok(row < 16 ? id0 : id1) && kTileKeys * u + row < Lk;
+        if (!ok) rv[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rv[i][c] = bf16x2_to_f16x2(rv[i][c], amax);
+      }
     }
+    if (kBf16 && !(amax < kF16Limit)) wide_s[u % kStages] = u;
+  };
+  auto store = [&](int u) {
+    const int st = u % kStages;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int idx = tid + i * NT;
+      const int row = idx >> 4, ch = idx & 15;
+      *reinterpret_cast<u32x4*>(&k_s[st][row][8 * ch]) = rk[i];
+      *reinterpret_cast<u32x4*>(&v_s[st][row][8 * ch]) = rv[i];
+    }
+  };
+  auto wide_at = [&](int u) -> bool {
+    return kBf16 && u < n_tiles && __builtin_amdgcn_readfirstlane(wide_s[u % kStages]) == u;
   };
 
-  if (n_tiles > 0) {
-    fetch_tile(0);
-    store_tile(0);
-  }
+  if (tid < kStages) wide_s[tid] = -1;
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) fetch_tile(t + 1);  // in flight during this tile's math
-    const int key0 = t * kTileKeys;
+  // Prologue: tile 0 into the ring, tile 1 in registers.
+  int t_id[2][2] = {{page_id(0), page_id(1)}, {page_id(2), page_id(3)}};  // page ids of tiles t, t+1
+  if (n_tiles > 0) {
+    issue(0, t_id[0][0], t_id[0][1]);
+    prepare(0, t_id[0][0], t_id[0][1]);
+  }
+  __syncthreads();
+  if (n_tiles > 0) store(0);
+  if (n_tiles > 1) {
+    issue(1, t_id[1][0], t_id[1][1]);
+    prepare(1, t_id[1][0], t_id[1][1]);
+  }
+  int id_n0 = page_id(4), id_n1 = page_id(5);  // page ids of the next tile to issue
+  __syncthreads();
+  bool wide = wide_at(0) || wide_at(1);
 
-    // S^T[key][column] for the tile's two 16-key blocks and every column block.
+  const float sl2 = a.scale_log2;
+  const uint32_t ones_f16 = 0x3C003C00u;
+
+  // One tile of the loop: (a) tile t+1 from registers into the ring, (b) tile
+  // t+2 into registers, (c) tile t on this wave's columns, (d) tile t+2
+  // zeroed/converted/flagged, (e) barrier: the ring slot of tile t+1 and the
+  // flag of tile t+2 become visible.
+  auto step = [&](int t, auto compute) {
+    if (t + 1 < n_tiles) store(t + 1);
+    const int t2_id0 = id_n0, t2_id1 = id_n1;
+    if (t + 2 < n_tiles) {
+      issue(t + 2, t2_id0, t2_id1);
+      id_n0 = page_id(2 * (t + 3));
+      id_n1 = page_id(2 * (t + 3) + 1);
+    }
+    compute(t);
+    if (t + 2 < n_tiles) prepare(t + 2, t2_id0, t2_id1);
+    t_id[0][0] = t_id[1][0];
+    t_id[0][1] = t_id[1][1];
+    t_id[1][0] = t2_id0;
+    t_id[1][1] = t2_id1;
+    __syncthreads();
+    return wide_at(t + 2);
+  };
+
+  auto compute = [&](int t) {
+    const int st = t % kStages;
+    const int key0 = t * kTileKeys;
+    // S^T[key][column] for the tile's two 16-key blocks and both column blocks.
     f32x4 sacc[2][CB];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -180,47 +310,44 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(const PrefillArgs a)
       for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[buf][kb * 16 + i16][32 * s + 8 * kg]);
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[st][kb * 16 + i16][32 * s + 8 * kg]);
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = mfma16x16x32<DT>(ka, qb[cb][s], sacc[kb][cb]);
+        for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = mfma16x16x32<DT>(ka, qv[cb][s], sacc[kb][cb]);
       }
     }
-    int kvalid[2][4];
+    const bool pg0 = page_ok(t_id[0][0]), pg1 = page_ok(t_id[0][1]);
+    const bool full = pg0 && pg1 && key0 + kTileKeys <= Lk && key0 + kTileKeys - 1 <= wpos_min;
+    if (!full) {
+      // key kb*16 + 4kg + r is visible to a column iff it is below lim[kb]
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int cb = 0; cb < CB; ++cb) {
+        const int vis = min(Lk, qpos[cb] + 1);
+        const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis : 0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) kvalid[kb][r] = valid_s[buf][kb * 16 + 4 * kg + r];
-
-    // V B-operands: lane (i16, kg) reads keys 4kg..4kg+3 and 16+4kg.. of dims 8*i16..+7.
-    u32x4 vr[2][4];
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vr[kb][r] = *reinterpret_cast<const u32x4*>(&v_s[buf][kb * 16 + 4 * kg + r][8 * i16]);
-
+          for (int r = 0; r < 4; ++r) {
+            const int key = key0 + kb * 16 + 4 * kg + r;
+            sacc[kb][cb][r] = key < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
+          }
+      }
+    }
+    // Softmax per column block: running max (rare rescale), p = 2^(s*scale*log2e - m) as fp16.
+    u32x4 pa[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      float s2[2][4];
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = key0 + kb * 16 + 4 * kg + r;
-          const bool ok = kvalid[kb][r] && key <= qpos[cb];
-          s2[kb][r] = ok ? sacc[kb][cb][r] * a.scale_log2 : -INFINITY;
-          mloc = fmaxf(mloc, s2[kb][r]);
-        }
-      if (__any(mloc > m_ref[cb] + kTau)) {
+      float mloc = fmaxf(fmaxf(fmaxf(sacc[0][cb][0], sacc[0][cb][1]), fmaxf(sacc[0][cb][2], sacc[0][cb][3])),
+                         fmaxf(fmaxf(sacc[1][cb][0], sacc[1][cb][1]), fmaxf(sacc[1][cb][2], sacc[1][cb][3])));
+      if (__any(mloc * sl2 > m_ref[cb] + kTau)) {
         float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
         mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
-        const float m_new = fmaxf(m_ref[cb], mcol);
+        const float m_new = fmaxf(m_ref[cb], mcol * sl2);
         const float alpha = fast_exp2(m_ref[cb] - m_new);
-        lsum[cb] *= alpha;
         m_ref[cb] = m_new;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * kg + r);
+          lacc[cb][r] *= ar;
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
         }
@@ -229,70 +356,72 @@ __global__ void __launch_bounds__(256) paged_prefill_kernel(const PrefillArgs a)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[kb][r] = fast_exp2(s2[kb][r] - m_ref[cb]);
-          lsum[cb] += p[kb][r];
-        }
-      const u32x4 pa = {pack2<DT>(p[0][0], p[0][1]), pack2<DT>(p[0][2], p[0][3]), pack2<DT>(p[1][0], p[1][1]),
-                        pack2<DT>(p[1][2], p[1][3])};
-      // bf16 keeps 8 significant bits of P: a second MFMA adds the rounding
-      // residual so that few-key rows stay within the fp32-accumulation
-      // tolerance (fp16 P keeps 11 bits and needs no residual).
-      u32x4 pl = {0u, 0u, 0u, 0u};
-      if constexpr (kSplitP) {
+        for (int r = 0; r < 4; ++r) p[kb][r] = fast_exp2(__builtin_fmaf(sacc[kb][cb][r], sl2, -m_ref[cb]));
+      pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
+                     pack_f16(p[1][2], p[1][3])};
+    }
+    // P.V: V B-operands for dims 8*i16 + 2c (lo) and + 2c + 1 (hi) over keys
+    // 4kg..4kg+3, 16+4kg..16+4kg+3, regrouped from 8-byte LDS row reads.
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float r0 = p[c >> 1][2 * (c & 1)] - __uint_as_float(pa[c] << 16);
-          const float r1 = p[c >> 1][2 * (c & 1) + 1] - __uint_as_float(pa[c] & 0xffff0000u);
-          pl[c] = pack2<DT>(r0, r1);
-        }
-      }
+    for (int h = 0; h < 2; ++h) {
+      u32x2 vr[2][4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 blo = {__builtin_amdgcn_perm(vr[0][1][c], vr[0][0][c], 0x05040100u),
-                           __builtin_amdgcn_perm(vr[0][3][c], vr[0][2][c], 0x05040100u),
-                           __builtin_amdgcn_perm(vr[1][1][c], vr[1][0][c], 0x05040100u),
-                           __builtin_amdgcn_perm(vr[1][3][c], vr[1][2][c], 0x05040100u)};
-        const u32x4 bhi = {__builtin_amdgcn_perm(vr[0][1][c], vr[0][0][c], 0x07060302u),
-                           __builtin_amdgcn_perm(vr[0][3][c], vr[0][2][c], 0x07060302u),
-                           __builtin_amdgcn_perm(vr[1][1][c], vr[1][0][c], 0x07060302u),
-                           __builtin_amdgcn_perm(vr[1][3][c], vr[1][2][c], 0x07060302u)};
-        o[cb][2 * c] = mfma16x16x32<DT>(pa, blo, o[cb][2 * c]);
-        o[cb][2 * c + 1] = mfma16x16x32<DT>(pa, bhi, o[cb][2 * c + 1]);
-        if constexpr (kSplitP) {
-          o[cb][2 * c] = mfma16x16x32<DT>(pl, blo, o[cb][2 * c]);
-          o[cb][2 * c + 1] = mfma16x16x32<DT>(pl, bhi, o[cb][2 * c + 1]);
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vr[kb][r] = *reinterpret_cast<const u32x2*>(&v_s[st][kb * 16 + 4 * kg + r][8 * i16 + 4 * h]);
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const u32x4 bl = {__builtin_amdgcn_perm(vr[0][1][cc], vr[0][0][cc], 0x05040100u),
+                          __builtin_amdgcn_perm(vr[0][3][cc], vr[0][2][cc], 0x05040100u),
+                          __builtin_amdgcn_perm(vr[1][1][cc], vr[1][0][cc], 0x05040100u),
+                          __builtin_amdgcn_perm(vr[1][3][cc], vr[1][2][cc], 0x05040100u)};
+        const u32x4 bh = {__builtin_amdgcn_perm(vr[0][1][cc], vr[0][0][cc], 0x07060302u),
+                          __builtin_amdgcn_perm(vr[0][3][cc], vr[0][2][cc], 0x07060302u),
+                          __builtin_amdgcn_perm(vr[1][1][cc], vr[1][0][cc], 0x07060302u),
+                          __builtin_amdgcn_perm(vr[1][3][cc], vr[1][2][cc], 0x07060302u)};
+        const int c = 2 * h + cc;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          o[cb][2 * c] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], bl, o[cb][2 * c]);
+          o[cb][2 * c + 1] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], bh, o[cb][2 * c + 1]);
         }
       }
     }
+    // Denominators: the same P against a ones operand.
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+      lacc[cb] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], u32x4{ones_f16, ones_f16, ones_f16, ones_f16}, lacc[cb]);
+  };
 
-    if (t + 1 < n_tiles) {
-      // Every wave finished reading buffer buf^1 before the barrier that ended
-      // the previous tile, so it can take tile t+1 now.
-      store_tile(buf ^ 1);
+  if (!wide) {
+    if (wave_live) {
+      for (int t = 0; t < n_tiles && !wide; ++t) wide = step(t, compute);
+    } else {
+      for (int t = 0; t < n_tiles && !wide; ++t) wide = step(t, [](int) {});
     }
-    __syncthreads();
+  }
+  if (kBf16 && wide) {
+    prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, q0, min(C, q0 + qw), wv, WAVES, lane);
+    return;
   }
 
-  // out[column] = o / l; the column sum of weights lives in lanes i16 = column.
+  // out[column] = o / l; lacc[cb][r] is the denominator of column 4*kg + r.
+  if (!wave_live) return;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    float lcol = lsum[cb] + __shfl_xor(lsum[cb], 16);
-    lcol += __shfl_xor(lcol, 32);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int col = 4 * kg + r;
-      const float lr = __shfl(lcol, col);
-      const int qi = q0 + (wv * CB + cb) * qpb + col / a.n_rep;
+      const int qi = wq0 + cb * qpb + col / a.n_rep;
       const int hh = g * a.n_rep + col % a.n_rep;
       if (qi < C && hh < a.Hq) {
-        float vals[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vals[e] = o[cb][e][r] / lr;
+        const float inv = 1.f / lacc[cb][r];
         u32x4 packed;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          packed[c] = uint32_t(Elem<DT>::from_float(vals[2 * c])) | (uint32_t(Elem<DT>::from_float(vals[2 * c + 1])) << 16);
+          packed[c] = uint32_t(Elem<DT>::from_float(o[cb][2 * c][r] * inv)) |
+                      (uint32_t(Elem<DT>::from_float(o[cb][2 * c + 1][r] * inv)) << 16);
         }
         *reinterpret_cast<u32x4*>(a.out + ((int64_t)(q_begin + qi) * a.Hq + hh) * D + 8 * i16) = packed;
       }
@@ -407,9 +536,6 @@ namespace {
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool mul8(int64_t x) { return (x & 7) == 0; }
 
-#ifndef UKV_PREFILL_CB
-#define UKV_PREFILL_CB 2
-#endif
 }  // namespace
 }  // namespace ukv
 
@@ -499,16 +625,19 @@ extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void*
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   const bool strides_ok = mul8(a.q_st) && mul8(a.q_sh) && mul8(a.k_sp) && mul8(a.k_st) && mul8(a.k_sh) &&
                           mul8(a.v_sp) && mul8(a.v_st) && mul8(a.v_sh);
-  const bool fast = head_dim == 128 && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
+  const bool fast = head_dim == 128 && softmax_scale > 0.f && std::isfinite(softmax_scale) && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
                     strides_ok && al16(q) && al16(out) && al16(k_cache) && al16(v_cache) && max_blocks > 0;
   if (fast) {
-    constexpr int CB = UKV_PREFILL_CB;
-    const int qw = 4 * CB * (16 / n_rep);
-    const dim3 grid((max_chunk + qw - 1) / qw, n_groups, batch);
+    constexpr int W = UKV_PREFILL_WAVES;
+    const int qw = W * kColBlocks * (16 / n_rep);
+    a.n_qblocks = (max_chunk + qw - 1) / qw;
+    const int64_t wgs = (int64_t)a.n_qblocks * n_groups * batch;
+    if (wgs == 0) return UKV_OK;
+    if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
     if (dtype == UKV_DTYPE_BF16)
-      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, CB>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
     else
-      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, CB>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
   } else {
     const dim3 grid(total_q, num_q_heads);
     if (dtype == UKV_DTYPE_BF16)
