@@ -37,6 +37,7 @@
 //     with v_perm_b32; the softmax denominators come from one more MFMA
 //     against a ones operand, so they sum exactly the rounded P.
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 #include "ukv_common.h"
@@ -83,12 +84,24 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float& amax) {
   return pack_f16(lo, hi);
 }
 
+// 8-byte LDS transpose read (ds_read_b64_tr_b16).
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 #ifndef UKV_PREFILL_WAVES
 #define UKV_PREFILL_WAVES 8
 #endif
 
 constexpr int kTileKeys = 32;
-constexpr int kRowPad = 136;  // LDS row pitch in 16-bit elements (128 + 8)
+// LDS row pitches in 16-bit elements. K rows (read 16 rows x 16 B per lane
+// group) sit 272 B apart, V rows (read as 4 rows x 32 B by the transpose
+// loads) 288 B apart, so that neither read pattern has bank conflicts.
+constexpr int kRowPad = 136;
+constexpr int kVRowPad = 144;
 constexpr int kStages = 3;
 constexpr int kColBlocks = 2;  // 16-column blocks per wave
 constexpr float kF16Limit = 65504.f;
@@ -145,8 +158,7 @@ paged_prefill_kernel(const PrefillArgs a) {
   constexpr bool kBf16 = DT == UKV_DTYPE_BF16;
   static_assert(ITEMS * NT == kTileKeys * 16, "loader mapping");
   __shared__ __attribute__((aligned(16))) uint16_t k_s[kStages][kTileKeys][kRowPad];
-  __shared__ __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kRowPad];  // fp16
-  __shared__ int wide_s[kStages];  // = tile index when that tile's bf16 V holds |v| >= 65520
+  __shared__ __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kVRowPad];  // fp16
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -194,113 +206,90 @@ paged_prefill_kernel(const PrefillArgs a) {
     for (int s = 0; s < STEPS; ++s) qv[cb][s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  float m_ref[CB];
+  float m_ref[CB], thr[CB];  // running max (log2 units) and the raw score that moves it
   f32x4 o[CB][8];
   f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     m_ref[cb] = kNegFltMax;
+    thr[cb] = -INFINITY;
     lacc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[cb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   // ---- tile loader: chunk idx = tid + i * NT is 16-byte chunk idx % 16 of key row idx / 16.
+  // Tile u is loaded into register set u & 1 three tiles ahead, written into
+  // ring slot u % 3 one tile ahead (zeroing rows past the sequence or on an
+  // invalid page and converting a bf16 V to fp16), and computed at tile u.
   const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
   auto page_id = [&](int pg) -> int { return pg < n_pg ? btrow[pg] : -1; };
   auto page_ok = [&](int id) -> bool { return (unsigned)id < (unsigned)a.num_pages; };
-  u32x4 rk[ITEMS], rv[ITEMS];
-  auto issue = [&](int u, int id0, int id1) {
+  // Within a page, this thread's chunk sits at a fixed offset; the page base is wave-uniform.
+  uint32_t koff[ITEMS], voff[ITEMS];
+  int lds_row[ITEMS], lds_ch[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int idx = tid + i * NT;
+    const int tok = (idx >> 4) & 15, ch = idx & 15;
+    koff[i] = (uint32_t)(tok * a.k_st + g * a.k_sh + 8 * ch);
+    voff[i] = (uint32_t)(tok * a.v_st + g * a.v_sh + 8 * ch);
+    lds_row[i] = idx >> 4;
+    lds_ch[i] = ch;
+  }
+  u32x4 rk0[ITEMS], rv0[ITEMS], rk1[ITEMS], rv1[ITEMS];
+  auto issue = [&](int id0, int id1, u32x4 (&rk)[ITEMS], u32x4 (&rv)[ITEMS]) {
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int idx = tid + i * NT;
-      const int row = idx >> 4, ch = idx & 15;
-      const int id = row < 16 ? id0 : id1;
-      const int pg = page_ok(id) ? id : 0;
-      const int tok = row & 15;
-      rk[i] = ld16(a.k + (int64_t)pg * a.k_sp + (int64_t)tok * a.k_st + (int64_t)g * a.k_sh + 8 * ch);
-      rv[i] = ld16(a.v + (int64_t)pg * a.v_sp + (int64_t)tok * a.v_st + (int64_t)g * a.v_sh + 8 * ch);
+      // rows 0-15 of a tile come from its first page, rows 16-31 from the second
+      const int second = __builtin_amdgcn_readfirstlane((tid + i * NT) >> 8);
+      const int id = second ? id1 : id0;
+      const int64_t pg = page_ok(id) ? id : 0;
+      rk[i] = ld16(a.k + pg * a.k_sp + koff[i]);
+      rv[i] = ld16(a.v + pg * a.v_sp + voff[i]);
     }
   };
-  // Zero V rows past the sequence or on an invalid page; a bf16 V becomes
-  // fp16, and a magnitude that fp16 cannot hold flags the tile.
-  auto prepare = [&](int u, int id0, int id1) {
+  bool wide_mine = false;  // this thread saw a bf16 V value fp16 cannot hold
+  auto store = [&](int u, int slot, int id0, int id1, u32x4 (&rk)[ITEMS], u32x4 (&rv)[ITEMS]) {
     const bool full = page_ok(id0) && page_ok(id1) && kTileKeys * (u + 1) <= Lk;
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int row = (tid + i * NT) >> 4;
+      u32x4 v = rv[i];
       if (!full) {
-        const bool ok = page_ok(row < 16 ? id0 : id1) && kTileKeys * u + row < Lk;
-        if (!ok) rv[i] = u32x4{0u, 0u, 0u, 0u};
+        const bool ok = page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk;
+        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
       }
       if constexpr (kBf16) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) rv[i][c] = bf16x2_to_f16x2(rv[i][c], amax);
+        for (int c = 0; c < 4; ++c) v[c] = bf16x2_to_f16x2(v[c], amax);
       }
+      *reinterpret_cast<u32x4*>(&k_s[slot][lds_row[i]][8 * lds_ch[i]]) = rk[i];
+      *reinterpret_cast<u32x4*>(&v_s[slot][lds_row[i]][8 * lds_ch[i]]) = v;
     }
-    if (kBf16 && !(amax < kF16Limit)) wide_s[u % kStages] = u;
+    if (kBf16) wide_mine |= !(amax < kF16Limit);
   };
-  auto store = [&](int u) {
-    const int st = u % kStages;
+
+  // Page ids of tiles t .. t+3 (t_id[j] = tile t + j).
+  int t_id[4][2];
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int idx = tid + i * NT;
-      const int row = idx >> 4, ch = idx & 15;
-      *reinterpret_cast<u32x4*>(&k_s[st][row][8 * ch]) = rk[i];
-      *reinterpret_cast<u32x4*>(&v_s[st][row][8 * ch]) = rv[i];
-    }
-  };
-  auto wide_at = [&](int u) -> bool {
-    return kBf16 && u < n_tiles && __builtin_amdgcn_readfirstlane(wide_s[u % kStages]) == u;
-  };
-
-  if (tid < kStages) wide_s[tid] = -1;
-  __syncthreads();
-
-  // Prologue: tile 0 into the ring, tile 1 in registers.
-  int t_id[2][2] = {{page_id(0), page_id(1)}, {page_id(2), page_id(3)}};  // page ids of tiles t, t+1
-  if (n_tiles > 0) {
-    issue(0, t_id[0][0], t_id[0][1]);
-    prepare(0, t_id[0][0], t_id[0][1]);
+  for (int j = 0; j < 4; ++j) {
+    t_id[j][0] = page_id(2 * j);
+    t_id[j][1] = page_id(2 * j + 1);
   }
+  // Prologue: tile 0 into the ring, tiles 1 and 2 in flight.
+  if (n_tiles > 0) issue(t_id[0][0], t_id[0][1], rk0, rv0);
+  if (n_tiles > 1) issue(t_id[1][0], t_id[1][1], rk1, rv1);
+  if (n_tiles > 0) store(0, 0, t_id[0][0], t_id[0][1], rk0, rv0);
+  if (n_tiles > 2) issue(t_id[2][0], t_id[2][1], rk0, rv0);
+  int id_n0 = page_id(8), id_n1 = page_id(9);  // page ids of tile t+4
   __syncthreads();
-  if (n_tiles > 0) store(0);
-  if (n_tiles > 1) {
-    issue(1, t_id[1][0], t_id[1][1]);
-    prepare(1, t_id[1][0], t_id[1][1]);
-  }
-  int id_n0 = page_id(4), id_n1 = page_id(5);  // page ids of the next tile to issue
-  __syncthreads();
-  bool wide = wide_at(0) || wide_at(1);
 
   const float sl2 = a.scale_log2;
+  const float inv_sl2 = 1.f / sl2;
   const uint32_t ones_f16 = 0x3C003C00u;
 
-  // One tile of the loop: (a) tile t+1 from registers into the ring, (b) tile
-  // t+2 into registers, (c) tile t on this wave's columns, (d) tile t+2
-  // zeroed/converted/flagged, (e) barrier: the ring slot of tile t+1 and the
-  // flag of tile t+2 become visible.
-  auto step = [&](int t, auto compute) {
-    if (t + 1 < n_tiles) store(t + 1);
-    const int t2_id0 = id_n0, t2_id1 = id_n1;
-    if (t + 2 < n_tiles) {
-      issue(t + 2, t2_id0, t2_id1);
-      id_n0 = page_id(2 * (t + 3));
-      id_n1 = page_id(2 * (t + 3) + 1);
-    }
-    compute(t);
-    if (t + 2 < n_tiles) prepare(t + 2, t2_id0, t2_id1);
-    t_id[0][0] = t_id[1][0];
-    t_id[0][1] = t_id[1][1];
-    t_id[1][0] = t2_id0;
-    t_id[1][1] = t2_id1;
-    __syncthreads();
-    return wide_at(t + 2);
-  };
-
-  auto compute = [&](int t) {
-    const int st = t % kStages;
+  auto compute = [&](int t, int slot) {
     const int key0 = t * kTileKeys;
     // S^T[key][column] for the tile's two 16-key blocks and both column blocks.
     f32x4 sacc[2][CB];
@@ -310,7 +299,7 @@ paged_prefill_kernel(const PrefillArgs a) {
       for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[st][kb * 16 + i16][32 * s + 8 * kg]);
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[slot][kb * 16 + i16][32 * s + 8 * kg]);
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = mfma16x16x32<DT>(ka, qv[cb][s], sacc[kb][cb]);
       }
@@ -321,15 +310,12 @@ paged_prefill_kernel(const PrefillArgs a) {
       // key kb*16 + 4kg + r is visible to a column iff it is below lim[kb]
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        const int vis = min(Lk, qpos[cb] + 1);
-        const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis : 0;
+        const int vis = min(Lk, qpos[cb] + 1) - key0 - 4 * kg;
+        const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis - 16 : 0;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = key0 + kb * 16 + 4 * kg + r;
-            sacc[kb][cb][r] = key < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
-          }
+          for (int r = 0; r < 4; ++r) sacc[kb][cb][r] = r < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
       }
     }
     // Softmax per column block: running max (rare rescale), p = 2^(s*scale*log2e - m) as fp16.
@@ -338,12 +324,13 @@ paged_prefill_kernel(const PrefillArgs a) {
     for (int cb = 0; cb < CB; ++cb) {
       float mloc = fmaxf(fmaxf(fmaxf(sacc[0][cb][0], sacc[0][cb][1]), fmaxf(sacc[0][cb][2], sacc[0][cb][3])),
                          fmaxf(fmaxf(sacc[1][cb][0], sacc[1][cb][1]), fmaxf(sacc[1][cb][2], sacc[1][cb][3])));
-      if (__any(mloc * sl2 > m_ref[cb] + kTau)) {
+      if (__any(mloc > thr[cb])) {
         float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
         mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
         const float m_new = fmaxf(m_ref[cb], mcol * sl2);
         const float alpha = fast_exp2(m_ref[cb] - m_new);
         m_ref[cb] = m_new;
+        thr[cb] = (m_new + kTau) * inv_sl2;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * kg + r);
@@ -360,33 +347,19 @@ paged_prefill_kernel(const PrefillArgs a) {
       pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                      pack_f16(p[1][2], p[1][3])};
     }
-    // P.V: V B-operands for dims 8*i16 + 2c (lo) and + 2c + 1 (hi) over keys
-    // 4kg..4kg+3, 16+4kg..16+4kg+3, regrouped from 8-byte LDS row reads.
+    // P.V: the B operand of output tile e (dims 16e .. 16e + 15) holds, in lane
+    // (i16, kg), dim 16e + i16 of keys 4kg..4kg+3 and 16+4kg..16+4kg+3 (the
+    // key order of P's A operand). ds_read_b64_tr_b16 builds it from row-major
+    // V: within each 16-lane group, lane L names 4 dims 4(L%4).. of key row
+    // L/4, and lane j receives dim j of the 4 rows.
+    const uint16_t* vlane = &v_s[slot][4 * kg + (i16 >> 2)][4 * (i16 & 3)];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x2 vr[2][4];
+    for (int e = 0; e < 8; ++e) {
+      const u32x2 lo = ds_read_tr16(vlane + 16 * e);
+      const u32x2 hi = ds_read_tr16(vlane + 16 * kVRowPad + 16 * e);
+      const u32x4 bv = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vr[kb][r] = *reinterpret_cast<const u32x2*>(&v_s[st][kb * 16 + 4 * kg + r][8 * i16 + 4 * h]);
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const u32x4 bl = {__builtin_amdgcn_perm(vr[0][1][cc], vr[0][0][cc], 0x05040100u),
-                          __builtin_amdgcn_perm(vr[0][3][cc], vr[0][2][cc], 0x05040100u),
-                          __builtin_amdgcn_perm(vr[1][1][cc], vr[1][0][cc], 0x05040100u),
-                          __builtin_amdgcn_perm(vr[1][3][cc], vr[1][2][cc], 0x05040100u)};
-        const u32x4 bh = {__builtin_amdgcn_perm(vr[0][1][cc], vr[0][0][cc], 0x07060302u),
-                          __builtin_amdgcn_perm(vr[0][3][cc], vr[0][2][cc], 0x07060302u),
-                          __builtin_amdgcn_perm(vr[1][1][cc], vr[1][0][cc], 0x07060302u),
-                          __builtin_amdgcn_perm(vr[1][3][cc], vr[1][2][cc], 0x07060302u)};
-        const int c = 2 * h + cc;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          o[cb][2 * c] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], bl, o[cb][2 * c]);
-          o[cb][2 * c + 1] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], bh, o[cb][2 * c + 1]);
-        }
-      }
+      for (int cb = 0; cb < CB; ++cb) o[cb][e] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], bv, o[cb][e]);
     }
     // Denominators: the same P against a ones operand.
 #pragma unroll
@@ -394,19 +367,54 @@ paged_prefill_kernel(const PrefillArgs a) {
       lacc[cb] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], u32x4{ones_f16, ones_f16, ones_f16, ones_f16}, lacc[cb]);
   };
 
-  if (!wide) {
-    if (wave_live) {
-      for (int t = 0; t < n_tiles && !wide; ++t) wide = step(t, compute);
-    } else {
-      for (int t = 0; t < n_tiles && !wide; ++t) wide = step(t, [](int) {});
+  // Tile t: (a) tile t+1 from register set (t+1)&1 into ring slot (t+1)%3;
+  // (b) tile t+3 into that register set; (c) tile t on this wave's columns;
+  // (d) barrier: slot (t+1)%3 becomes visible.
+  auto step = [&](int t, int slot, auto set_parity, auto do_compute) {
+    constexpr int P1 = decltype(set_parity)::value;  // parity of tile t+1
+    int nslot = slot + 1 == kStages ? 0 : slot + 1;
+    if (t + 1 < n_tiles) {
+      if constexpr (P1 == 0) store(t + 1, nslot, t_id[1][0], t_id[1][1], rk0, rv0);
+      else store(t + 1, nslot, t_id[1][0], t_id[1][1], rk1, rv1);
     }
-  }
-  if (kBf16 && wide) {
+    if (t + 3 < n_tiles) {
+      if constexpr (P1 == 0) issue(t_id[3][0], t_id[3][1], rk0, rv0);
+      else issue(t_id[3][0], t_id[3][1], rk1, rv1);
+    }
+    do_compute(t, slot);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      t_id[j][0] = t_id[j + 1][0];
+      t_id[j][1] = t_id[j + 1][1];
+    }
+    t_id[3][0] = id_n0;
+    t_id[3][1] = id_n1;
+    id_n0 = page_id(2 * (t + 5));
+    id_n1 = page_id(2 * (t + 5) + 1);
+    __syncthreads();
+    return nslot;
+  };
+  using Even = std::integral_constant<int, 0>;
+  using Odd = std::integral_constant<int, 1>;
+  auto run = [&](auto do_compute) {
+    int slot = 0;
+    for (int t = 0; t < n_tiles; t += 2) {
+      slot = step(t, slot, Odd{}, do_compute);  // tile t+1 is odd
+      if (t + 1 < n_tiles) slot = step(t + 1, slot, Even{}, do_compute);
+    }
+  };
+  if (wave_live) run(compute);
+  else run([](int, int) {});
+
+  // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
+  // recompute its columns on the fp32 fallback.
+  if (kBf16 && __syncthreads_or(wide_mine)) {
     prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, q0, min(C, q0 + qw), wv, WAVES, lane);
     return;
   }
 
-  // out[column] = o / l; lacc[cb][r] is the denominator of column 4*kg + r.
+  // out[column] = o / l: lane (i16, kg) holds dims 16e + i16 of columns 4*kg + r,
+// and lacc[cb][r] is the denominator of column 4*kg + r.
   if (!wave_live) return;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -417,13 +425,9 @@ paged_prefill_kernel(const PrefillArgs a) {
       const int hh = g * a.n_rep + col % a.n_rep;
       if (qi < C && hh < a.Hq) {
         const float inv = 1.f / lacc[cb][r];
-        u32x4 packed;
+        uint16_t* orow = a.out + ((int64_t)(q_begin + qi) * a.Hq + hh) * D + i16;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          packed[c] = uint32_t(Elem<DT>::from_float(o[cb][2 * c][r] * inv)) |
-                      (uint32_t(Elem<DT>::from_float(o[cb][2 * c + 1][r] * inv)) << 16);
-        }
-        *reinterpret_cast<u32x4*>(a.out + ((int64_t)(q_begin + qi) * a.Hq + hh) * D + 8 * i16) = packed;
+        for (int e = 0; e < 8; ++e) orow[16 * e] = Elem<DT>::from_float(o[cb][e][r] * inv);
       }
     }
   }
