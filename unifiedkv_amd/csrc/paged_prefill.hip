@@ -76,12 +76,28 @@ __device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t w) { return __builtin_bit_cast(u16x2, w); }
+
 // Two bf16 values -> two fp16 values (RNE; exact when 2^-14 <= |x| < 65520),
-// folding |x| into amax.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float& amax) {
-  const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xffff0000u);
-  amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
-  return pack_f16(lo, hi);
+// folding the magnitude bits of both into amag (bf16 magnitudes above 0x477F,
+// i.e. |x| >= 65536, inf and NaN, do not fit fp16).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, u16x2& amag) {
+  amag = __builtin_elementwise_max(amag, as_u16x2(w & 0x7fff7fffu));
+  return pack_f16(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
+// Tile loads whose completion the kernel waits for itself. Two register sets
+// are in flight while a tile is computed; the compiler's own wait placement
+// cannot see which set is older across the unrolled loop and waits for both,
+// so the loads are issued here and vm_wait<N>() waits until at most N vector
+// memory operations are outstanding. The "+v" operands make every use of the
+// loaded registers follow the wait.
+__device__ __forceinline__ void gload16(u32x4& r, const void* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(r) : "v"(p));
+}
+template <int N> __device__ __forceinline__ void vm_wait(u32x4& x, u32x4& y) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(x), "+v"(y) : "n"(N));
 }
 
 // 8-byte LDS transpose read (ds_read_b64_tr_b16).
@@ -104,7 +120,6 @@ constexpr int kRowPad = 136;
 constexpr int kVRowPad = 144;
 constexpr int kStages = 3;
 constexpr int kColBlocks = 2;  // 16-column blocks per wave
-constexpr float kF16Limit = 65504.f;
 
 // Fallback for a workgroup whose key range holds a bf16 V value of magnitude
 // >= 65520 (or infinite), which fp16 cannot carry: every (query, head) pair
@@ -206,13 +221,12 @@ paged_prefill_kernel(const PrefillArgs a) {
     for (int s = 0; s < STEPS; ++s) qv[cb][s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  float m_ref[CB], thr[CB];  // running max (log2 units) and the raw score that moves it
+  float m_ref[CB];  // running max of the column (log2 units)
   f32x4 o[CB][8];
   f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     m_ref[cb] = kNegFltMax;
-    thr[cb] = -INFINITY;
     lacc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[cb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -222,7 +236,11 @@ paged_prefill_kernel(const PrefillArgs a) {
   // Tile u is loaded into register set u & 1 three tiles ahead, written into
   // ring slot u % 3 one tile ahead (zeroing rows past the sequence or on an
   // invalid page and converting a bf16 V to fp16), and computed at tile u.
-  const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
+  // The block table is read through the constant address space: the kernel
+  // never writes it, and this keeps the wave-uniform page-id loads on the
+  // scalar unit (SMEM), apart from the vector-memory count the tile loads use.
+  typedef const __attribute__((address_space(4))) int32_t cint32;
+  cint32* btrow = (cint32*)(a.bt + (int64_t)b * a.max_blocks);
   auto page_id = [&](int pg) -> int { return pg < n_pg ? btrow[pg] : -1; };
   auto page_ok = [&](int id) -> bool { return (unsigned)id < (unsigned)a.num_pages; };
   // Within a page, this thread's chunk sits at a fixed offset; the page base is wave-uniform.
@@ -245,29 +263,32 @@ paged_prefill_kernel(const PrefillArgs a) {
       const int second = __builtin_amdgcn_readfirstlane((tid + i * NT) >> 8);
       const int id = second ? id1 : id0;
       const int64_t pg = page_ok(id) ? id : 0;
-      rk[i] = ld16(a.k + pg * a.k_sp + koff[i]);
-      rv[i] = ld16(a.v + pg * a.v_sp + voff[i]);
+      gload16(rk[i], a.k + pg * a.k_sp + koff[i]);
+      gload16(rv[i], a.v + pg * a.v_sp + voff[i]);
     }
   };
   bool wide_mine = false;  // this thread saw a bf16 V value fp16 cannot hold
   auto store = [&](int u, int slot, int id0, int id1, u32x4 (&rk)[ITEMS], u32x4 (&rv)[ITEMS]) {
     const bool full = page_ok(id0) && page_ok(id1) && kTileKeys * (u + 1) <= Lk;
-    float amax = 0.f;
+    u16x2 amag = {0, 0};
+    // The other register set's 2 * ITEMS loads were issued after this set's.
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) vm_wait<2 * ITEMS>(rk[i], rv[i]);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      u32x4 v = rv[i];
-      if (!full) {
-        const bool ok = page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk;
-        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-      }
+      const bool ok = full || (page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk);
+      const u32x4 v0 = rv[i];
+      u32x4 v;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = ok ? v0[c] : 0u;
       if constexpr (kBf16) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = bf16x2_to_f16x2(v[c], amax);
+        for (int c = 0; c < 4; ++c) v[c] = bf16x2_to_f16x2(v[c], amag);
       }
       *reinterpret_cast<u32x4*>(&k_s[slot][lds_row[i]][8 * lds_ch[i]]) = rk[i];
       *reinterpret_cast<u32x4*>(&v_s[slot][lds_row[i]][8 * lds_ch[i]]) = v;
     }
-    if (kBf16) wide_mine |= !(amax < kF16Limit);
+    if (kBf16) wide_mine |= __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(amag, u16x2{0x477F, 0x477F})) != 0u;
   };
 
   // Page ids of tiles t .. t+3 (t_id[j] = tile t + j).
@@ -277,16 +298,20 @@ paged_prefill_kernel(const PrefillArgs a) {
     t_id[j][0] = page_id(2 * j);
     t_id[j][1] = page_id(2 * j + 1);
   }
-  // Prologue: tile 0 into the ring, tiles 1 and 2 in flight.
-  if (n_tiles > 0) issue(t_id[0][0], t_id[0][1], rk0, rv0);
-  if (n_tiles > 1) issue(t_id[1][0], t_id[1][1], rk1, rv1);
-  if (n_tiles > 0) store(0, 0, t_id[0][0], t_id[0][1], rk0, rv0);
-  if (n_tiles > 2) issue(t_id[2][0], t_id[2][1], rk0, rv0);
+  // Prologue: tile 0 into the ring, tiles 1 and 2 in flight. Loads are issued
+  // unconditionally (tiles past the end read page 0 and are never used) so
+  // that every wait is on loads of a fixed age: vmcnt(2) on the older set.
+  issue(t_id[0][0], t_id[0][1], rk0, rv0);
+  issue(t_id[1][0], t_id[1][1], rk1, rv1);
+  store(0, 0, t_id[0][0], t_id[0][1], rk0, rv0);
+  issue(t_id[2][0], t_id[2][1], rk0, rv0);
   int id_n0 = page_id(8), id_n1 = page_id(9);  // page ids of tile t+4
+  // Retire every load issued so far (q columns, tiles 1 and 2) once, so that
+  // no wait for them is left inside the loop.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
   const float sl2 = a.scale_log2;
-  const float inv_sl2 = 1.f / sl2;
   const uint32_t ones_f16 = 0x3C003C00u;
 
   auto compute = [&](int t, int slot) {
@@ -318,27 +343,13 @@ paged_prefill_kernel(const PrefillArgs a) {
           for (int r = 0; r < 4; ++r) sacc[kb][cb][r] = r < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
       }
     }
-    // Softmax per column block: running max (rare rescale), p = 2^(s*scale*log2e - m) as fp16.
+    // Softmax: p = 2^(s*scale*log2e - m) as fp16 against the running max m
+    // (log2 units) of its column. m moves only when some p of the tile reaches
+    // 2^8: the packed fp16 P is checked (non-negative fp16 bit patterns order
+    // like their values, and inf and NaN lie above), and a column block whose
+    // max moved is rescaled and its P recomputed.
     u32x4 pa[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      float mloc = fmaxf(fmaxf(fmaxf(sacc[0][cb][0], sacc[0][cb][1]), fmaxf(sacc[0][cb][2], sacc[0][cb][3])),
-                         fmaxf(fmaxf(sacc[1][cb][0], sacc[1][cb][1]), fmaxf(sacc[1][cb][2], sacc[1][cb][3])));
-      if (__any(mloc > thr[cb])) {
-        float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
-        const float m_new = fmaxf(m_ref[cb], mcol * sl2);
-        const float alpha = fast_exp2(m_ref[cb] - m_new);
-        m_ref[cb] = m_new;
-        thr[cb] = (m_new + kTau) * inv_sl2;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha, 4 * kg + r);
-          lacc[cb][r] *= ar;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
-        }
-      }
+    auto exp_pack = [&](int cb) {
       float p[2][4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -346,6 +357,38 @@ paged_prefill_kernel(const PrefillArgs a) {
         for (int r = 0; r < 4; ++r) p[kb][r] = fast_exp2(__builtin_fmaf(sacc[kb][cb][r], sl2, -m_ref[cb]));
       pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                      pack_f16(p[1][2], p[1][3])};
+    };
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) exp_pack(cb);
+    u16x2 pmax = as_u16x2(pa[0][0]);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) pmax = __builtin_elementwise_max(pmax, as_u16x2(pa[cb][c]));
+    if (__any(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(pmax, u16x2{0x5BFF, 0x5BFF})) != 0u)) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        float mloc = sacc[0][cb][0];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[kb][cb][r]);
+        float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
+        if (__any(mcol * sl2 > m_ref[cb] + kTau)) {
+          const float m_new = fmaxf(m_ref[cb], mcol * sl2);
+          const float alpha = fast_exp2(m_ref[cb] - m_new);
+          m_ref[cb] = m_new;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * kg + r);
+            lacc[cb][r] *= ar;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
+          }
+          exp_pack(cb);
+        }
+      }
     }
     // P.V: the B operand of output tile e (dims 16e .. 16e + 15) holds, in lane
     // (i16, kg), dim 16e + i16 of keys 4kg..4kg+3 and 16+4kg..16+4kg+3 (the
@@ -373,14 +416,11 @@ paged_prefill_kernel(const PrefillArgs a) {
   auto step = [&](int t, int slot, auto set_parity, auto do_compute) {
     constexpr int P1 = decltype(set_parity)::value;  // parity of tile t+1
     int nslot = slot + 1 == kStages ? 0 : slot + 1;
-    if (t + 1 < n_tiles) {
-      if constexpr (P1 == 0) store(t + 1, nslot, t_id[1][0], t_id[1][1], rk0, rv0);
-      else store(t + 1, nslot, t_id[1][0], t_id[1][1], rk1, rv1);
-    }
-    if (t + 3 < n_tiles) {
-      if constexpr (P1 == 0) issue(t_id[3][0], t_id[3][1], rk0, rv0);
-      else issue(t_id[3][0], t_id[3][1], rk1, rv1);
-    }
+    // (a slot written past the last tile is never read)
+    if constexpr (P1 == 0) store(t + 1, nslot, t_id[1][0], t_id[1][1], rk0, rv0);
+    else store(t + 1, nslot, t_id[1][0], t_id[1][1], rk1, rv1);
+    if constexpr (P1 == 0) issue(t_id[3][0], t_id[3][1], rk0, rv0);
+    else issue(t_id[3][0], t_id[3][1], rk1, rv1);
     do_compute(t, slot);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
@@ -405,6 +445,13 @@ paged_prefill_kernel(const PrefillArgs a) {
   };
   if (wave_live) run(compute);
   else run([](int, int) {});
+  // Loads of tiles past the end are still in flight: retire them while their
+  // registers are still held, so that nothing else is placed in them first.
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    vm_wait<0>(rk0[i], rv0[i]);
+    vm_wait<0>(rk1[i], rv1[i]);
+  }
 
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
