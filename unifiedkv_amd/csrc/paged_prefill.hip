@@ -20,8 +20,8 @@
 //     8 XCDs) runs consecutive work items: the query blocks of one (sequence,
 //     group) share that XCD's L2 while they stream the same pages;
 //   * key tiles of 32 keys (two pages) pass through registers into a 3-stage
-//     LDS ring (rows padded to 272 B), one barrier per tile; the loads of tile
-//     t+2 are in flight while tile t is computed;
+//     LDS ring (rows padded to 288 B), one barrier per tile; the loads of
+//     tiles t+2 and t+3 are in flight while tile t is computed;
 //   * S^T = K Q^T on v_mfma_f32_16x16x32 in the input type (A = 16 keys x 32
 //     dims from LDS, B = the wave's q columns in registers); lane l ends with
 //     keys 4*(l/16) + r of column l % 16;
@@ -113,11 +113,18 @@ __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
 #endif
 
 constexpr int kTileKeys = 32;
-// LDS row pitches in 16-bit elements. K rows (read 16 rows x 16 B per lane
-// group) sit 272 B apart, V rows (read as 4 rows x 32 B by the transpose
-// loads) 288 B apart, so that neither read pattern has bank conflicts.
-constexpr int kRowPad = 136;
-constexpr int kVRowPad = 144;
+// LDS row pitches in 16-bit elements: K and V rows sit 288 B apart, the pitch
+// at which SQ_LDS_BANK_CONFLICT reads 0 for the 16-row x 16-byte K reads, the
+// 4-row x 32-byte V transpose reads and the 16-byte row stores (272 B leaves
+// the K reads conflicting).
+#ifndef UKV_PREFILL_KPAD
+#define UKV_PREFILL_KPAD 144
+#endif
+#ifndef UKV_PREFILL_VPAD
+#define UKV_PREFILL_VPAD 144
+#endif
+constexpr int kRowPad = UKV_PREFILL_KPAD;
+constexpr int kVRowPad = UKV_PREFILL_VPAD;
 constexpr int kStages = 3;
 constexpr int kColBlocks = 2;  // 16-column blocks per wave
 
