@@ -115,7 +115,8 @@ def check(actual, exp, what):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("prefix,chunk", [([0], [37]), ([100, 16], [64, 16]), ([333, 0, 48], [5, 70, 1]),
-                                          ([2000], [300]), ([17], [129])])
+                                          ([2000], [300]), ([17], [129]), ([50, 20], [0, 9]), ([15], [1]),
+                                          ([31], [33]), ([64, 1], [64, 63]), ([4000], [17])])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_prefill_matches_oracle(cuda, prefix, chunk, dtype):
     case = make_case(sum(prefix) + sum(chunk), prefix, chunk, dtype=dtype)
