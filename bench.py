@@ -24,6 +24,9 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
   --workload offload           config 5b: evicted pages -> pinned host -> new pages
   --workload compacted_decode  config 5c: decode B=8 at L=6704 on the compacted tables,
                                rotating through the 32 layers
+  --workload step              a 32-layer decode step on the config-2 batch: prologue + fused
+                               append/decode per layer, beside the unfused kernels and the
+                               reference's call pattern (step_ragged: the config-3 batch)
   --workload prefill           config 4: chunked prefill, 4 x (16384 prefix + 2048 chunk),
                                TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak
 """
@@ -224,6 +227,137 @@ def run_decode(args, dev):
     case = workloads.numpy_decode_case(layout, args.seed)
     tc = workloads.to_torch(case, dev)
     return decode_record(layout, tc, args, "page16_decode_config1_tiny", "Page16 decode GB/s, config 1 tiny B=4 fp16")
+
+
+# ------------------------------------------------------------------- 32-layer decode step
+def run_step(args, dev):
+    """One decode step of a 32-layer model over the config-2 (or config-3) batch: the step's
+    prologue (new pages + attention lengths, once) and per layer the fused append + decode.
+    Beside it, on the same pool and batch: the same kernels unfused (append kernel, then
+    decode), and the reference's call pattern (core/scheduler.py:1092-1160, 401-418: per-row
+    table uploads per layer, torch index_put of the token, attn_lens = old + 1) with this
+    build's decode kernel, so the difference is the prologue's and the fusion's."""
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd import page16_native, page_ops, workloads
+    from unifiedkv_amd.decode_step import DecodeBatch
+    from unifiedkv_amd.pool import PagedKVPool
+
+    n_layers = 32
+    rng = np.random.default_rng(args.seed)
+    ragged = args.workload == "step_ragged"
+    layout = workloads.layout_ragged(rng) if ragged else workloads.layout_longctx(rng)
+    B, Hq, Hkv, D = layout["B"], layout["Hq"], layout["Hkv"], layout["D"]
+    lens0 = [int(x) for x in layout["seqlens"]]
+    lists0 = [[int(x) for x in layout["block_table"][b, : (L + 15) // 16]] for b, L in enumerate(lens0)]
+    # Room for the pages the timed steps add (one per sequence per 16 steps, three variants).
+    total_steps = 3 * (args.warmup + 2 * args.steps)
+    N = int(layout["N"]) + B * (total_steps // 16 + 2)
+    pool = PagedKVPool(16, n_layers, Hkv, D, torch.bfloat16, num_blocks=N, device=dev)
+    used = set(x for ids in lists0 for x in ids)
+    pool.allocate_blocks(N)
+    pool.free_blocks_by_ids([i for i in range(N) if i not in used])
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    for l in range(n_layers):
+        pool.k_cache[l].normal_(generator=g)
+        pool.v_cache[l].normal_(generator=g)
+    qs = [torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_layers)]
+    kns = [torch.randn((B, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_layers)]
+    vns = [torch.randn((B, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_layers)]
+    scale, n_rep = D ** -0.5, Hq // Hkv
+    log(f"[bench] step: {n_layers} layers, pool {N} pages/layer "
+        f"({2 * pool.k_cache.numel() * 2 / 2**30:.1f} GiB)")
+
+    # (a) prologue + fused append/decode
+    fused = DecodeBatch(pool, [list(x) for x in lists0], lens0)
+    lens_log = []
+
+    def step_fused():
+        lens_log.append(fused.seq_lens)
+        fused.begin_step()
+        for l in range(n_layers):
+            fused.attention(l, qs[l], kns[l], vns[l], softmax_scale=scale, n_rep=n_rep)
+        fused.end_step()
+
+    fused_ms, _ = event_time_ms(step_fused, args.steps, args.warmup)
+    mean_len = float(np.mean([np.mean(x) for x in lens_log])) + 1.0
+    log(f"[bench] step fused: {fused_ms * 1e3:.1f} us")
+
+    # (b) prologue + append kernel + decode per layer
+    unfused = DecodeBatch(pool, [list(x) for x in lists0], lens0)
+
+    def step_unfused():
+        bt, attn = unfused.begin_step()
+        for l in range(n_layers):
+            unfused.append(l, kns[l], vns[l])
+            page16_native.page16_decode_attention(qs[l], pool.k_cache[l], pool.v_cache[l], bt, attn,
+                                                  softmax_scale=scale, n_rep=n_rep)
+        unfused.end_step()
+
+    unfused_ms, _ = event_time_ms(step_unfused, args.steps, args.warmup)
+    log(f"[bench] step unfused: {unfused_ms * 1e3:.1f} us")
+
+    # (c) the reference's call pattern with this build's decode kernel
+    ref_lists = [list(x) for x in lists0]
+    ref_lens = list(lens0)
+
+    def step_reference_pattern():
+        for i, L in enumerate(ref_lens):  # reserve_decode_slot (core/offload.py:838-866)
+            if L % 16 == 0:
+                ref_lists[i].extend(pool.allocate_blocks(1))
+        cache_seqlens = torch.tensor(ref_lens, dtype=torch.int32, device=dev)
+        width = max(len(ids) for ids in ref_lists)
+        for l in range(n_layers):
+            bt = torch.zeros(B, width, dtype=torch.int32, device=dev)  # core/pool.py:174-189
+            for i, ids in enumerate(ref_lists):
+                bt[i, : len(ids)] = torch.tensor(ids, dtype=torch.int32, device=dev)
+            batch_idx = torch.arange(B, device=dev, dtype=torch.long)  # core/scheduler.py:401-408
+            block_pos = torch.div(cache_seqlens.to(torch.long), 16, rounding_mode="floor")
+            tok_pos = torch.remainder(cache_seqlens.to(torch.long), 16)
+            block_ids = bt[batch_idx, block_pos]
+            pool.k_cache[l][block_ids.to(torch.long), tok_pos, :, :] = kns[l]
+            pool.v_cache[l][block_ids.to(torch.long), tok_pos, :, :] = vns[l]
+            attn_lens = (cache_seqlens + 1).to(dtype=torch.int32)
+            page16_native.page16_decode_attention(qs[l], pool.k_cache[l], pool.v_cache[l], bt, attn_lens,
+                                                  softmax_scale=scale, n_rep=n_rep)
+        for i in range(B):  # commit (core/scheduler.py:1247-1265)
+            ref_lens[i] += 1
+
+    ref_steps = max(3, args.steps // 4)
+    ref_ms, _ = event_time_ms(step_reference_pattern, ref_steps, max(1, args.warmup // 4))
+    log(f"[bench] step reference pattern: {ref_ms * 1e3:.1f} us")
+
+    max_blocks = int(fused.block_table.shape[1])
+    layer_bytes = workloads.decode_bytes(np.full(B, mean_len), B, Hq, Hkv, D, max_blocks) + 2 * B * Hkv * D * 2
+    step_bytes = n_layers * layer_bytes
+    gbps = step_bytes / (fused_ms * 1e-3) / 1e9
+    name = "config3_ragged" if ragged else "config2_longctx"
+    return {
+        "metric": f"Decode step over 32 layers (prologue + fused append/decode), {name}, tokens/s",
+        "value": round(B / (fused_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(fused_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool, q and new K/V rows; random-permutation block tables)",
+        "config": {"workload": f"decode_step_32_layers_{name}", "layers": n_layers, "batch": B,
+                   "start_lengths_mean": float(np.mean(lens0)), "num_q_heads": Hq, "num_kv_heads": Hkv,
+                   "head_dim": D, "page_size": 16, "pool_pages_per_layer": N},
+        "us_per_step": {"fused": round(fused_ms * 1e3, 1), "unfused_append_then_decode": round(unfused_ms * 1e3, 1),
+                        "reference_call_pattern": round(ref_ms * 1e3, 1)},
+        "us_per_layer_saved_vs_reference_pattern": round((ref_ms - fused_ms) * 1e3 / n_layers, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "note": "whole step: 32 x (KV pages read + token rows written) / step time"},
+        "cpu_baseline": None,
+    }
 
 
 # ---------------------------------------------------------------------------------- config 5
@@ -524,7 +658,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill"])
+                    choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill",
+                             "step", "step_ragged"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -567,6 +702,8 @@ def main():
         rec = run_offload(args, dev)
     elif args.workload == "prefill":
         rec = run_prefill(args, dev)
+    elif args.workload in ("step", "step_ragged"):
+        rec = run_step(args, dev)
     else:
         rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)

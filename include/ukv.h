@@ -16,6 +16,10 @@
  *                          core/offload.py:1236-1262 prune_sequence_window (pool->pool compaction),
  *                          core/offload.py:163-179, 577-597, 662-680 per-page offload/prefetch copies
  *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
+ *   ukv_page16_decode_append  core/scheduler.py:401-418 that scatter fused with the decode call
+ *   ukv_decode_prologue    core/offload.py:780-866 reserve_decode_slot (table side),
+ *                          core/scheduler.py:1092-1160 per-layer table / cache_seqlens build,
+ *                          core/scheduler.py:1247-1265 commit (seq_len += 1)
  *   ukv_select_topk        core/scheduler.py:613-616, core/compress.py:141-142 block top-k + sort
  *   ukv_kv_write_varlen    core/pool.py:127-141 for a prefill chunk appended after its prefix
  *   ukv_paged_prefill      core/engine.py:1826-1854 chunked prefill attention over past KV
@@ -92,6 +96,25 @@ int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
                       int dtype, void* workspace, size_t workspace_bytes, ukv_stream_t stream);
 
 /*
+ * Decode with the step's token append fused in: the same result as ukv_kv_append with
+ * old_lens = seqlens - 1 (block_size 16) followed by ukv_page16_decode over seqlens, in one
+ * call. k_new / v_new are [batch, num_kv_heads, head_dim] rows with element strides
+ * new_strides[0..1] = {batch, head}; the token of sequence b is written to position
+ * seqlens[b] - 1 unless seqlens[b] <= 0, the position is beyond max_blocks * 16 or its page
+ * id is outside [0, num_pages). The split kernel writes the rows itself while it reads that
+ * page (one launch fewer per layer); shapes it does not take run the append kernel first.
+ * Workspace as for ukv_page16_decode. Replaces core/scheduler.py:401-418 (block_pos / tok_pos,
+ * the K and V index_put, attn_lens = old_lens + 1, page16_decode_attention).
+ */
+int ukv_page16_decode_append(const void* q, void* k_cache, void* v_cache, const int32_t* block_table,
+                             const int32_t* seqlens, const void* k_new, const void* v_new,
+                             const int64_t* new_strides, void* out, int batch, int num_q_heads,
+                             int num_kv_heads, int head_dim, int n_rep, int max_blocks, int num_pages,
+                             const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                             float softmax_scale, int dtype, void* workspace, size_t workspace_bytes,
+                             ukv_stream_t stream);
+
+/*
  * Token rows <-> pages for one layer of the pool (bit-exact copies).
  *   pool_layer   [num_pages, block_size, num_heads, head_dim], element strides pool_strides[0..2]
  *                (page, token, head); last dimension contiguous
@@ -136,6 +159,22 @@ int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strid
                   const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
                   int max_blocks, const int32_t* old_lens, int32_t* new_lens, int batch, int block_size,
                   int num_heads, int head_dim, int num_pages, ukv_stream_t stream);
+
+/*
+ * Once per decode step, shared by every layer (the table and lengths are the same for all
+ * layers): writes the step's new pages into the device block table and the attention
+ * lengths. new_pages is a HOST array of n_new (row, col, page id) int32 triples; each sets
+ * block_table[row * max_blocks + col] = page id. Every row must be in [0, batch) and every
+ * col in [0, max_blocks), else UKV_ERR_INVALID_ARGUMENT and nothing is launched. If lens_out
+ * is not NULL, lens_out[b] = lens_in[b] + 1 for b < batch (lens_out may equal lens_in). The
+ * triples travel as kernel arguments (no host-to-device copy; one launch per 128 triples).
+ * Replaces the table side of core/offload.py:780-866 (reserve_decode_slot: the new block
+ * id appended to every layer's gpu_block_map), the per-layer build_block_table and
+ * cache_seqlens of core/scheduler.py:1092-1160, and the seq_len += 1 loop of
+ * core/scheduler.py:1247-1265.
+ */
+int ukv_decode_prologue(int32_t* block_table, int max_blocks, int batch, const int32_t* lens_in,
+                        int32_t* lens_out, const int32_t* new_pages, int n_new, ukv_stream_t stream);
 
 /*
  * Retain-set selection: for each row r, the k_r indices i < n_r with the largest scores

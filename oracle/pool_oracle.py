@@ -7,6 +7,10 @@ Only tests/ may import this module. Each function follows the cited lines of BP-
 * ``read_kv_from_blocks``  core/pool.py:154-172
 * ``build_block_table``    core/pool.py:174-189 (zero padded int32 [B, max_len])
 * ``kv_append``            core/scheduler.py:401-408 (token at len -> page bt[b, len//16], slot len%16)
+* ``reserve_decode_slots`` core/offload.py:838-866 per sequence in batch order (core/scheduler.py:1101-1104):
+                           len % 16 == 0 -> one FIFO page appended to the sequence's block list
+* ``decode_steps``         the page16_native decode loop: reserve, per layer table + append + attention
+                           over old_len + 1 (core/scheduler.py:1092-1160, 401-418), commit (1247-1265)
 * ``pool_size``            core/pool.py:36-45 (N_total from free memory)
 
 Caches here are numpy arrays [N, 16, H, D] of one layer (any dtype; the copies are bit-exact).
@@ -107,3 +111,37 @@ def kv_append(k_cache: np.ndarray, v_cache: np.ndarray, block_table: np.ndarray,
     k_cache[block_ids.astype(np.int64), tok_pos] = k_new
     v_cache[block_ids.astype(np.int64), tok_pos] = v_new
     return (old_lens + 1).astype(np.int32)
+
+
+def reserve_decode_slots(allocator, page_lists, seq_lens, block_size: int = 16):
+    """Returns the page given to each sequence this step (None where none was needed); page_lists
+    are extended in place. Raises like the reference with no page to evict."""
+    got = []
+    for i, L in enumerate(seq_lens):
+        if int(L) % block_size == 0:
+            new_ids = allocator.allocate_blocks(1)
+            if not new_ids:
+                raise RuntimeError("page16_native_blocked:direct_decode_expand_evict_failed")
+            page_lists[i].extend(new_ids)
+            got.append(int(new_ids[0]))
+        else:
+            got.append(None)
+    return got
+
+
+def decode_steps(allocator, k_pool, v_pool, page_lists, seq_lens, tokens, attend, block_size: int = 16):
+    """k_pool / v_pool: per-layer lists of [N, 16, H, D] arrays (modified in place);
+    tokens[step][layer] = (q, k_new, v_new) with k_new / v_new [B, H, D];
+    attend(layer, q, block_table, attn_lens) -> output. Returns (outputs[step][layer], seq_lens)."""
+    lens = np.asarray(seq_lens, dtype=np.int32).copy()
+    outs = []
+    for step_tokens in tokens:
+        reserve_decode_slots(allocator, page_lists, lens, block_size)
+        bt = build_block_table(page_lists)
+        row = []
+        for layer, (q, k_new, v_new) in enumerate(step_tokens):
+            attn_lens = kv_append(k_pool[layer], v_pool[layer], bt, lens, k_new, v_new, block_size)
+            row.append(attend(layer, q, bt, attn_lens))
+        outs.append(row)
+        lens = lens + 1
+    return outs, lens

@@ -124,6 +124,35 @@ def test_zero_length_gives_nan_and_overlong_is_clamped(cuda):
     assert_close(out, exp, "zero / clamped lengths")
 
 
+def test_stale_workspace_with_fewer_pages_than_workgroups(cuda):
+    # A wide table with short sequences: B * max_blocks / 8 split workgroups but only 10
+    # pages, so most workgroups own no page and write no partial. The workspace is
+    # pre-filled with garbage (huge finite values, NaN, zeros) that must never be read.
+    from unifiedkv_amd import _ext
+
+    torch = _torch()
+    lens = [20, 30, 16, 17, 1, 0, 33]
+    B, Hq, Hkv, D, mb = len(lens), 32, 8, 128, 256
+    case = custom_case(41, B, Hq, Hkv, D, lens, max_blocks=mb)
+    tc = workloads.to_torch(case)
+    exp = expected_dense(case)
+    lib = _ext.load()
+    ws_bytes = int(lib.ukv_page16_workspace_bytes(B, Hq, D, mb))
+    for fill in (0x7F, 0xFF, 0x00):
+        ws = torch.full((ws_bytes,), fill, dtype=torch.uint8, device=cuda)
+        out = torch.empty_like(tc["q"])
+        rc = lib.ukv_page16_decode(
+            tc["q"].data_ptr(), tc["k_cache"].data_ptr(), tc["v_cache"].data_ptr(), tc["block_table"].data_ptr(),
+            tc["seqlens"].data_ptr(), out.data_ptr(), B, Hq, Hkv, D, Hq // Hkv, mb, case["N"],
+            _ext.i64_array(tc["q"].stride()[:2]), _ext.i64_array(tc["k_cache"].stride()[:3]),
+            _ext.i64_array(tc["v_cache"].stride()[:3]), case["scale"], _ext.UKV_DTYPE_BF16, ws.data_ptr(), ws_bytes,
+            torch.cuda.current_stream().cuda_stream)
+        assert rc == _ext.UKV_OK
+        got = to_f32(out)
+        assert np.isnan(got[5]).all()
+        assert_close(got, exp, f"stale workspace filled with {fill:#x}")
+
+
 def test_invalid_page_ids_are_masked(cuda):
     case = custom_case(24, 2, 32, 8, 128, [64, 48])
     case["block_table"] = case["block_table"].copy()

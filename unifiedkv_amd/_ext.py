@@ -77,6 +77,27 @@ SIGNATURES = {
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # batch, block_size, heads, head_dim, pages, stream
         ],
     ),
+    "ukv_page16_decode_append": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p,  # q, k_cache, v_cache
+            _c_void_p, _c_void_p,  # block_table, seqlens
+            _c_void_p, _c_void_p, _c_i64p, _c_void_p,  # k_new, v_new, new strides, out
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # batch, Hq, Hkv, D, n_rep
+            _c_int, _c_int,  # max_blocks, num_pages
+            _c_i64p, _c_i64p, _c_i64p,  # q/k/v strides
+            ctypes.c_float, _c_int,  # softmax_scale, dtype
+            _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "ukv_decode_prologue": (
+        _c_int,
+        [
+            _c_void_p, _c_int, _c_int,  # block_table, max_blocks, batch
+            _c_void_p, _c_void_p,  # lens_in, lens_out
+            ctypes.POINTER(ctypes.c_int32), _c_int, _c_void_p,  # host (row, col, id) triples, n_new, stream
+        ],
+    ),
     "ukv_kv_write_varlen": (
         _c_int,
         [

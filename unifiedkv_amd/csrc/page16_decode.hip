@@ -53,6 +53,11 @@ struct DecodeArgs {
   int64_t v_sp, v_st, v_sh;
   int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
   int grid_wgs;      // G: workgroups sharing the batch's pages
+  // Decode-token append (fused variant): k_new/v_new [B][n_groups][D] rows with
+  // strides n_sb, n_sh; the token of sequence b goes to position lens[b] - 1.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t n_sb, n_sh;
   float scale;       // natural-log units (scalar kernel)
   float scale_log2;  // scale * log2(e) (split kernel)
 };
@@ -144,6 +149,17 @@ __device__ __forceinline__ u32x2 ld8_stream(const uint16_t* p) {
 template <int DPL> struct VRow { uint32_t w[DPL / 2]; };
 
 template <int DPL>
+__device__ __forceinline__ void store_vrow(uint16_t* p, const VRow<DPL>& r) {
+  if constexpr (DPL == 4) {
+    *reinterpret_cast<u32x2*>(p) = u32x2{r.w[0], r.w[1]};
+  } else {
+#pragma unroll
+    for (int c = 0; c < DPL / 8; ++c)
+      *reinterpret_cast<u32x4*>(p + 8 * c) = u32x4{r.w[4 * c], r.w[4 * c + 1], r.w[4 * c + 2], r.w[4 * c + 3]};
+  }
+}
+
+template <int DPL>
 __device__ __forceinline__ void load_vrow(const uint16_t* p, VRow<DPL>& r) {
   if constexpr (DPL == 4) {
     const u32x2 x = ld8_stream(p);
@@ -175,7 +191,16 @@ __device__ __forceinline__ void load_vrow(const uint16_t* p, VRow<DPL>& r) {
 //         Result tile e: lane l holds O[head 4*kg + r][dim DPL*i16 + e].
 // The running max is only moved when a score exceeds it by more than 2^8
 // (log2 units; weights stay <= 256), decided by a wave-wide vote.
-template <int DT, int D>
+//
+// APPEND: the decode token of sequence b (position lens[b] - 1) is taken from
+// k_new/v_new instead of the pool. The wave that owns the page holding it loads
+// the new K/V rows into registers of their own when its segment starts, swaps
+// them in for the page's stale slot when that page is reduced, and stores them
+// into the pool after its page loop (no memory operation is added inside the
+// pipelined loop). Every (page, KV head) is read by exactly one wave, so each
+// token row is written once, and the attention sees the same values as an
+// append followed by a plain decode.
+template <int DT, int D, bool APPEND>
 __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PER_EU) page16_split_kernel(const DecodeArgs a) {
   constexpr int STEPS = D / 32;  // QK k-steps of 32 dims
   constexpr int DPL = D / 16;    // V dims per lane = P.V output tiles
@@ -241,6 +266,11 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
   int pb = 0;        // one past the last page
   const int32_t* btrow = nullptr;
   int bid_win = 0;   // page ids pa + 64*k + lane of the current 64-page window
+  int tail_page = -1;  // APPEND: page of the decode token if this segment holds it, else -1
+  int tail_slot = 0;   // APPEND: its slot in that page
+  int tail_pid = -1;   // APPEND: that page's id, -1 if invalid
+  u32x4 ktok[STEPS];   // APPEND: the new K row (lanes i16 == tail_slot)
+  VRow<DPL> vtok;      // APPEND: the new V row (lanes kg == tail_slot / 4)
 
   u32x4 qb[STEPS];   // B operand of QK^T: column i16 = q head qh0 + i16 (zero beyond n_here)
   float m_ref;       // running max of head i16 (log2 units)
@@ -252,6 +282,8 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
     if (idx != 0 && (idx & 63) == 0) bid_win = (p + lane < pb) ? btrow[p + lane] : 0;
     int bid = __builtin_amdgcn_readlane(bid_win, idx & 63);
     const bool ok = (unsigned)bid < (unsigned)a.num_pages;
+    if constexpr (APPEND)
+      if (p == tail_page) tail_pid = ok ? bid : -1;
     bid = ok ? bid : 0;
     nv = ok ? min(16, L - 16 * p) : 0;
     const uint16_t* kp = kbase + (int64_t)bid * a.k_sp;
@@ -260,6 +292,18 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
     const uint16_t* vp = vbase + (int64_t)bid * a.v_sp;
 #pragma unroll
     for (int t = 0; t < 4; ++t) load_vrow<DPL>(vp + (int64_t)t * a.v_st, vr[t]);
+  };
+
+  // APPEND: on the token's page, its slot gets the new rows (per-lane register selects).
+  auto swap_in_token = [&](u32x4 (&kr)[STEPS], VRow<DPL> (&vr)[4]) {
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) kr[s] = (i16 == tail_slot) ? ktok[s] : kr[s];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool mine = 4 * kg + t == tail_slot;
+#pragma unroll
+      for (int c = 0; c < DPL / 2; ++c) vr[t].w[c] = mine ? vtok.w[c] : vr[t].w[c];
+    }
   };
 
   auto process_page = [&](const u32x4 (&kr)[STEPS], VRow<DPL> (&vr)[4], int nv) {
@@ -328,6 +372,20 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
     pb = min(x1, seg_start + n_b) - seg_start;
     btrow = a.bt + (int64_t)b * a.max_blocks;
     bid_win = (pa + lane < pb) ? btrow[pa + lane] : 0;
+    if constexpr (APPEND) {
+      // A length beyond the table is clamped; its token has no slot and is not written.
+      tail_page = (L > 0 && L == a.lens[b]) ? ((L - 1) >> 4) : -1;
+      if (tail_page < pa || tail_page >= pb) tail_page = -1;  // another workgroup's page
+      tail_pid = -1;
+      if (tail_page >= 0) {
+        tail_slot = (L - 1) & 15;
+        const uint16_t* kn = a.k_new + (int64_t)b * a.n_sb + (int64_t)g * a.n_sh;
+        const uint16_t* vn = a.v_new + (int64_t)b * a.n_sb + (int64_t)g * a.n_sh;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) ktok[s] = ld16(kn + 8 * kg + 32 * s);
+        load_vrow<DPL>(vn + DPL * i16, vtok);
+      }
+    }
     {
       const uint16_t* qp = a.q + (int64_t)b * a.q_sb + (int64_t)(qh0 + (live ? i16 : 0)) * a.q_sh + 8 * kg;
 #pragma unroll
@@ -350,8 +408,23 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
         if (p < pb) {
           const int nxt = (u + kPipe - 1) % kPipe;  // constant after unrolling
           if (p + kPipe - 1 < pb) load_page(p + kPipe - 1, kb[nxt], vb[nxt], nvb[nxt]);
+          if constexpr (APPEND)
+            if (p == tail_page) swap_in_token(kb[u], vb[u]);
           process_page(kb[u], vb[u], nvb[u]);
         }
+      }
+    }
+
+    if constexpr (APPEND) {
+      if (tail_pid >= 0) {  // the token's page is valid: write its rows into the pool
+        if (i16 == tail_slot) {
+          uint16_t* kd = const_cast<uint16_t*>(kbase) + (int64_t)tail_pid * a.k_sp;
+#pragma unroll
+          for (int s = 0; s < STEPS; ++s) *reinterpret_cast<u32x4*>(kd + 32 * s) = ktok[s];
+        }
+        if (kg == (tail_slot >> 2))
+          store_vrow<DPL>(const_cast<uint16_t*>(vbase) + (int64_t)tail_pid * a.v_sp + (int64_t)(tail_slot & 3) * a.v_st,
+                          vtok);
       }
     }
 
@@ -421,12 +494,23 @@ __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a)
   const int w_last = n_pages > 0 ? (int)(((S + n_pages) * G - 1) / P) : -1;
   const int n_chunks = w_last - w_first + 1;
   const int64_t base = (int64_t)(w_first + b) * a.Hq + h;
+  // With fewer pages than workgroups (P < G) some workgroups in [w_first, w_last]
+  // own no page and wrote no partial: their slots hold stale data and are skipped.
+  auto owns_pages = [&](int c) {
+    const int64_t w = w_first + c;
+    return ((w + 1) * P) / G > (w * P) / G;
+  };
 
   float mx = -INFINITY;
-  for (int c = tid; c < n_chunks; c += 256) mx = fmaxf(mx, a.part_ml[base + (int64_t)c * a.Hq].x);
+  for (int c = tid; c < n_chunks; c += 256)
+    if (owns_pages(c)) mx = fmaxf(mx, a.part_ml[base + (int64_t)c * a.Hq].x);
   const float M = block_reduce_256(mx, red, true);
   float dsum = 0.f;
   for (int c = tid; c < n_chunks; c += 256) {
+    if (!owns_pages(c)) {
+      w_s[c] = -1.f;  // marks an empty slot (real weights are >= 0 or NaN)
+      continue;
+    }
     const float2 ml = a.part_ml[base + (int64_t)c * a.Hq];
     const float w = exp2f(ml.x - M);
     w_s[c] = w;
@@ -441,9 +525,8 @@ __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a)
   const int64_t cstride = (int64_t)a.Hq * D;
 #pragma unroll 4
   for (int c = cs; c < n_chunks; c += CS) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(po + (int64_t)c * cstride);
     const float w = w_s[c];
-    acc += w * v;
+    if (!(w < 0.f)) acc += w * *reinterpret_cast<const f32x4*>(po + (int64_t)c * cstride);
   }
   float* sums = w_s + ((a.grid_wgs + 3) & ~3);
   *reinterpret_cast<f32x4*>(sums + cs * D + 4 * dq) = acc;
@@ -568,7 +651,10 @@ template <int DT, int D>
 void launch_split(const DecodeArgs& a, hipStream_t stream) {
   const int waves = std::min(UKV_PAGE16_WAVES, a.n_groups);
   const dim3 grid(a.grid_wgs, 1, (a.n_groups + waves - 1) / waves);
-  hipLaunchKernelGGL((page16_split_kernel<DT, D>), grid, dim3(64 * waves), 0, stream, a);
+  if (a.k_new)
+    hipLaunchKernelGGL((page16_split_kernel<DT, D, true>), grid, dim3(64 * waves), 0, stream, a);
+  else
+    hipLaunchKernelGGL((page16_split_kernel<DT, D, false>), grid, dim3(64 * waves), 0, stream, a);
 }
 
 template <int DT>
@@ -610,12 +696,21 @@ extern "C" size_t ukv_page16_workspace_bytes(int batch, int num_q_heads, int hea
   return workspace_layout(batch, num_q_heads, head_dim, max_blocks).total;
 }
 
-extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
-                                 const int32_t* block_table, const int32_t* seqlens, void* out, int batch,
-                                 int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks,
-                                 int num_pages, const int64_t* q_strides, const int64_t* k_strides,
-                                 const int64_t* v_strides, float softmax_scale, int dtype, void* workspace,
-                                 size_t workspace_bytes, ukv_stream_t stream_handle) {
+namespace {
+
+// The decode token of the fused entry point: rows k_new[b], v_new[b] of
+// [batch][num_kv_heads][head_dim] with element strides new_strides[0..1].
+struct TokenRows {
+  const void* k;
+  const void* v;
+  const int64_t* strides;
+};
+
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                const int32_t* seqlens, void* out, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                int n_rep, int max_blocks, int num_pages, const int64_t* q_strides, const int64_t* k_strides,
+                const int64_t* v_strides, float softmax_scale, int dtype, void* workspace, size_t workspace_bytes,
+                ukv_stream_t stream_handle, const TokenRows* tok) {
   if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0) return UKV_ERR_EMPTY;
   if (head_dim > 256) return UKV_ERR_HEAD_DIM;
   if (dtype != UKV_DTYPE_F16 && dtype != UKV_DTYPE_BF16) return UKV_ERR_DTYPE;
@@ -625,6 +720,7 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
   if (max_blocks < 0 || num_pages < 0) return UKV_ERR_INVALID_ARGUMENT;
   if (!q || !out || !seqlens || !q_strides || !k_strides || !v_strides) return UKV_ERR_INVALID_ARGUMENT;
   if (max_blocks > 0 && (!block_table || !k_cache || !v_cache || num_pages <= 0)) return UKV_ERR_INVALID_ARGUMENT;
+  if (tok && (!tok->k || !tok->v || !tok->strides)) return UKV_ERR_INVALID_ARGUMENT;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   DecodeArgs a{};
@@ -656,16 +752,36 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
                           (a.k_sh % 8 == 0) && (a.v_sp % 8 == 0) && (a.v_st % 8 == 0) && (a.v_sh % 8 == 0);
   const bool fast = (head_dim == 64 || head_dim == 128 || head_dim == 256) && n_rep <= 16 && strides_ok &&
                     aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) && max_blocks > 0;
+  // The split kernel writes the token itself when every KV head is read by
+  // some wave and the new rows are 16-byte aligned; otherwise the append runs
+  // as its own kernel first.
+  const bool fused = tok && fast && n_groups == num_kv_heads && aligned16(tok->k) && aligned16(tok->v) &&
+                     tok->strides[0] % 8 == 0 && tok->strides[1] % 8 == 0;
+  WorkspaceLayout w{};
+  if (fast) {
+    w = workspace_layout(batch, num_q_heads, head_dim, max_blocks);
+    if (!workspace || workspace_bytes < w.total || !aligned16(workspace)) return UKV_ERR_WORKSPACE;
+  }
+  if (tok && !fused && max_blocks > 0) {
+    const int rc = append_decode_rows(const_cast<void*>(k_cache), const_cast<void*>(v_cache), k_strides, v_strides,
+                                      tok->k, tok->v, tok->strides, block_table, max_blocks, seqlens, -1, nullptr,
+                                      batch, 16, num_kv_heads, head_dim, num_pages, stream);
+    if (rc != UKV_OK) return rc;
+  }
 
   if (fast) {
-    const WorkspaceLayout w = workspace_layout(batch, num_q_heads, head_dim, max_blocks);
-    if (!workspace || workspace_bytes < w.total || !aligned16(workspace)) return UKV_ERR_WORKSPACE;
     char* ws = static_cast<char*>(workspace);
     a.part_o = reinterpret_cast<float*>(ws + w.part_o_off);
     a.part_ml = reinterpret_cast<float2*>(ws + w.part_ml_off);
     a.seq_start = reinterpret_cast<int32_t*>(ws + w.seq_off);
     a.seq_pages = a.seq_start + batch;
     a.grid_wgs = w.wgs;
+    if (fused) {
+      a.k_new = static_cast<const uint16_t*>(tok->k);
+      a.v_new = static_cast<const uint16_t*>(tok->v);
+      a.n_sb = tok->strides[0];
+      a.n_sh = tok->strides[1];
+    }
     const bool launched =
         dtype == UKV_DTYPE_BF16 ? dispatch_split<UKV_DTYPE_BF16>(a, stream) : dispatch_split<UKV_DTYPE_F16>(a, stream);
     if (!launched) return UKV_ERR_LAUNCH;
@@ -680,4 +796,30 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
   }
   if (hipGetLastError() != hipSuccess) return UKV_ERR_LAUNCH;
   return UKV_OK;
+}
+
+}  // namespace
+
+extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* block_table, const int32_t* seqlens, void* out, int batch,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks,
+                                 int num_pages, const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, float softmax_scale, int dtype, void* workspace,
+                                 size_t workspace_bytes, ukv_stream_t stream_handle) {
+  return decode_impl(q, k_cache, v_cache, block_table, seqlens, out, batch, num_q_heads, num_kv_heads, head_dim,
+                     n_rep, max_blocks, num_pages, q_strides, k_strides, v_strides, softmax_scale, dtype, workspace,
+                     workspace_bytes, stream_handle, nullptr);
+}
+
+extern "C" int ukv_page16_decode_append(const void* q, void* k_cache, void* v_cache, const int32_t* block_table,
+                                        const int32_t* seqlens, const void* k_new, const void* v_new,
+                                        const int64_t* new_strides, void* out, int batch, int num_q_heads,
+                                        int num_kv_heads, int head_dim, int n_rep, int max_blocks, int num_pages,
+                                        const int64_t* q_strides, const int64_t* k_strides,
+                                        const int64_t* v_strides, float softmax_scale, int dtype, void* workspace,
+                                        size_t workspace_bytes, ukv_stream_t stream_handle) {
+  const TokenRows tok{k_new, v_new, new_strides};
+  return decode_impl(q, k_cache, v_cache, block_table, seqlens, out, batch, num_q_heads, num_kv_heads, head_dim,
+                     n_rep, max_blocks, num_pages, q_strides, k_strides, v_strides, softmax_scale, dtype, workspace,
+                     workspace_bytes, stream_handle, &tok);
 }

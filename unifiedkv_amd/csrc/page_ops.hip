@@ -7,6 +7,9 @@
 //                          (core/scheduler.py:702-733, core/offload.py:1236-1262, 577-597, 662-680)
 //   ukv_kv_append          the decode step's new K/V token into page bt[b, len/bs], slot len%bs
 //                          (core/scheduler.py:401-408)
+//   ukv_decode_prologue    once per decode step: the step's new page ids into the block table and
+//                          the attention lengths lens + 1 (core/offload.py:780-866,
+//                          core/scheduler.py:1092-1160, 1247-1265)
 //
 // All of them are HBM-bound copies of 16-byte chunks; every byte is read once and written once.
 // Rows must be 16-byte aligned (D % 8 == 0 and aligned strides); a 2-byte element path covers
@@ -107,6 +110,7 @@ struct AppendArgs {
   const int32_t* block_table;
   int max_blocks;
   const int32_t* old_lens;
+  int pos_offset;     // the token of sequence b goes to position old_lens[b] + pos_offset
   int32_t* new_lens;  // nullable: old_lens + 1
   int B, H, D, num_pages, bs;
   int vec;  // rows 16-byte aligned: copy 16-byte chunks
@@ -115,8 +119,9 @@ struct AppendArgs {
 // grid (B); the block writes one token row of every head of sequence b.
 __global__ void __launch_bounds__(256) kv_append_kernel(const AppendArgs a) {
   const int b = blockIdx.x;
-  const int len = a.old_lens[b];
-  if (threadIdx.x == 0 && a.new_lens) a.new_lens[b] = len + 1;
+  const int lv = a.old_lens[b];
+  if (threadIdx.x == 0 && a.new_lens) a.new_lens[b] = lv + 1;
+  const int len = lv + a.pos_offset;
   if (len < 0) return;
   const int blk = len / a.bs;
   if (blk >= a.max_blocks) return;
@@ -139,6 +144,30 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const AppendArgs a) {
       *vd = a.v_new[src];
     }
   }
+}
+
+// Kernel arguments carry up to kPrologueMax (row, col, page id) triples, so a
+// decode step's new pages reach the table without a host-to-device copy.
+constexpr int kPrologueMax = 128;
+
+struct PrologueArgs {
+  int32_t* bt;
+  int max_blocks;
+  int B;
+  const int32_t* lens_in;
+  int32_t* lens_out;  // nullable
+  int n;
+  int32_t trip[3 * kPrologueMax];
+};
+
+// One block: threads write the new table entries, then every sequence's
+// attention length. lens_in may alias lens_out (each thread reads, then writes,
+// its own element).
+__global__ void __launch_bounds__(256) decode_prologue_kernel(const PrologueArgs a) {
+  const int t = threadIdx.x;
+  if (t < a.n) a.bt[(int64_t)a.trip[3 * t] * a.max_blocks + a.trip[3 * t + 1]] = a.trip[3 * t + 2];
+  if (a.lens_out)
+    for (int b = t; b < a.B; b += blockDim.x) a.lens_out[b] = a.lens_in[b] + 1;
 }
 
 namespace {
@@ -259,16 +288,17 @@ extern "C" int ukv_page_copy(const void* const* src_pools, void* const* dst_pool
   return UKV_OK;
 }
 
-extern "C" int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides,
-                             const int64_t* v_strides, const void* k_new, const void* v_new,
-                             const int64_t* new_strides, const int32_t* block_table, int max_blocks,
-                             const int32_t* old_lens, int32_t* new_lens, int batch, int block_size,
-                             int num_heads, int head_dim, int num_pages, ukv_stream_t stream) {
+namespace ukv {
+
+int append_decode_rows(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides, const int64_t* v_strides,
+                       const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
+                       int max_blocks, const int32_t* lens, int pos_offset, int32_t* new_lens, int batch,
+                       int block_size, int num_heads, int head_dim, int num_pages, ukv_stream_t stream) {
   if (batch < 0 || num_heads <= 0 || head_dim <= 0 || max_blocks < 0 || block_size <= 0)
     return UKV_ERR_INVALID_ARGUMENT;
   if (batch == 0) return UKV_OK;
-  if (!k_pool_layer || !v_pool_layer || !k_strides || !v_strides || !k_new || !v_new || !new_strides ||
-      !old_lens || (max_blocks > 0 && !block_table))
+  if (!k_pool_layer || !v_pool_layer || !k_strides || !v_strides || !k_new || !v_new || !new_strides || !lens ||
+      (max_blocks > 0 && !block_table))
     return UKV_ERR_INVALID_ARGUMENT;
   AppendArgs a{};
   a.k_pool = static_cast<uint16_t*>(k_pool_layer);
@@ -285,7 +315,8 @@ extern "C" int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64
   a.n_sh = new_strides[1];
   a.block_table = block_table;
   a.max_blocks = max_blocks;
-  a.old_lens = old_lens;
+  a.old_lens = lens;
+  a.pos_offset = pos_offset;
   a.new_lens = new_lens;
   a.B = batch;
   a.H = num_heads;
@@ -297,4 +328,43 @@ extern "C" int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64
           m8(a.n_sh);
   hipLaunchKernelGGL(kv_append_kernel, dim3(batch), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
+}
+
+}  // namespace ukv
+
+extern "C" int ukv_kv_append(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides,
+                             const int64_t* v_strides, const void* k_new, const void* v_new,
+                             const int64_t* new_strides, const int32_t* block_table, int max_blocks,
+                             const int32_t* old_lens, int32_t* new_lens, int batch, int block_size,
+                             int num_heads, int head_dim, int num_pages, ukv_stream_t stream) {
+  return append_decode_rows(k_pool_layer, v_pool_layer, k_strides, v_strides, k_new, v_new, new_strides,
+                            block_table, max_blocks, old_lens, 0, new_lens, batch, block_size, num_heads, head_dim,
+                            num_pages, stream);
+}
+
+extern "C" int ukv_decode_prologue(int32_t* block_table, int max_blocks, int batch, const int32_t* lens_in,
+                                   int32_t* lens_out, const int32_t* new_pages, int n_new, ukv_stream_t stream) {
+  if (batch < 0 || max_blocks < 0 || n_new < 0) return UKV_ERR_INVALID_ARGUMENT;
+  if (n_new > 0 && (!new_pages || !block_table)) return UKV_ERR_INVALID_ARGUMENT;
+  if (lens_out && batch > 0 && !lens_in) return UKV_ERR_INVALID_ARGUMENT;
+  // The triples are host memory: validate every one before launching anything.
+  for (int i = 0; i < n_new; ++i) {
+    const int32_t row = new_pages[3 * i], col = new_pages[3 * i + 1];
+    if (row < 0 || row >= batch || col < 0 || col >= max_blocks) return UKV_ERR_INVALID_ARGUMENT;
+  }
+  const bool lens = lens_out && batch > 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int i0 = 0; i0 < n_new || (i0 == 0 && lens); i0 += kPrologueMax) {
+    PrologueArgs a{};
+    a.bt = block_table;
+    a.max_blocks = max_blocks;
+    a.B = batch;
+    a.lens_in = lens_in;
+    a.lens_out = (i0 == 0 && lens) ? lens_out : nullptr;
+    a.n = std::min(kPrologueMax, std::max(0, n_new - i0));
+    std::copy(new_pages + 3 * i0, new_pages + 3 * (i0 + a.n), a.trip);
+    hipLaunchKernelGGL(decode_prologue_kernel, dim3(1), dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return UKV_ERR_LAUNCH;
+  }
+  return UKV_OK;
 }

@@ -107,4 +107,13 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Host side, page_ops.hip: writes row b of k_new/v_new ([batch][num_heads][head_dim],
+// strides new_strides[0..1]) at position lens[b] + pos_offset of sequence b (page
+// block_table[b][pos / block_size], slot pos % block_size); positions outside the table
+// and invalid page ids are skipped. new_lens (nullable) receives lens + 1.
+int append_decode_rows(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides, const int64_t* v_strides,
+                       const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
+                       int max_blocks, const int32_t* lens, int pos_offset, int32_t* new_lens, int batch,
+                       int block_size, int num_heads, int head_dim, int num_pages, ukv_stream_t stream);
+
 }  // namespace ukv

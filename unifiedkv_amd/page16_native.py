@@ -39,26 +39,9 @@ def _status_message(code: int, head_dim: int) -> str:
     return f"page16_native_runtime_error:{_ext.status_string(code)}"
 
 
-def page16_decode_attention(
-    q: torch.Tensor,
-    k_cache: torch.Tensor,
-    v_cache: torch.Tensor,
-    block_table: torch.Tensor,
-    cache_seqlens: torch.Tensor,
-    *,
-    softmax_scale: float,
-    n_rep: int,
-) -> torch.Tensor:
-    """Decode-only paged attention over 16-token blocks.
-
-    Args:
-        q: [batch, num_q_heads, head_dim] fp16/bf16 device tensor.
-        k_cache/v_cache: [num_blocks, 16, num_kv_heads, head_dim], last dim contiguous.
-        block_table: [batch, max_blocks] int32 device tensor (zero padded).
-        cache_seqlens: [batch] device tensor, including the current token.
-
-    Same contract as core/page16_native.py:83-150; q head h reads KV head h // n_rep.
-    """
+def _prepare(q, k_cache, v_cache, block_table, cache_seqlens):
+    """The reference's argument checks, in its order (core/page16_native.py:101-124),
+    then the native kernels' own; returns the normalised call arguments."""
     if not HAS_TRITON:
         raise RuntimeError("page16_native_unavailable:triton_not_available")
     if q.dim() != 3:
@@ -101,13 +84,42 @@ def page16_decode_attention(
         block_table = block_table.to(torch.int32)
     block_table = block_table.contiguous()
     cache_seqlens = cache_seqlens.to(dtype=torch.int32).contiguous()
+    return q, block_table, cache_seqlens, batch, num_q_heads, num_kv_heads, head_dim, dev
+
+
+def _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev) -> torch.Tensor:
+    ws_bytes = int(lib.ukv_page16_workspace_bytes(batch, num_q_heads, head_dim, max_blocks))
+    return torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+
+
+def page16_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    *,
+    softmax_scale: float,
+    n_rep: int,
+) -> torch.Tensor:
+    """Decode-only paged attention over 16-token blocks.
+
+    Args:
+        q: [batch, num_q_heads, head_dim] fp16/bf16 device tensor.
+        k_cache/v_cache: [num_blocks, 16, num_kv_heads, head_dim], last dim contiguous.
+        block_table: [batch, max_blocks] int32 device tensor (zero padded).
+        cache_seqlens: [batch] device tensor, including the current token.
+
+    Same contract as core/page16_native.py:83-150; q head h reads KV head h // n_rep.
+    """
+    q, block_table, cache_seqlens, batch, num_q_heads, num_kv_heads, head_dim, dev = _prepare(
+        q, k_cache, v_cache, block_table, cache_seqlens)
     out = torch.empty_like(q)
     max_blocks = int(block_table.shape[1])
     num_pages = min(int(k_cache.shape[0]), int(v_cache.shape[0]))
 
     lib = _ext.load()
-    ws_bytes = int(lib.ukv_page16_workspace_bytes(batch, num_q_heads, head_dim, max_blocks))
-    workspace = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    workspace = _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     code = lib.ukv_page16_decode(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -125,4 +137,61 @@ def page16_decode_attention(
     return out
 
 
-__all__ = ["HAS_TRITON", "HAS_UKV", "page16_decode_attention"]
+def page16_decode_append_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    *,
+    softmax_scale: float,
+    n_rep: int,
+) -> torch.Tensor:
+    """The decode step's token append and ``page16_decode_attention`` in one call.
+
+    ``cache_seqlens`` are the attention lengths (old lengths + 1, as passed to the
+    decode call); ``k_new``/``v_new`` are the step's [batch, num_kv_heads, head_dim]
+    (or [batch, 1, num_kv_heads, head_dim]) rows, written to position
+    cache_seqlens[b] - 1 of sequence b before it is attended. Same result and pool
+    contents as core/scheduler.py:401-418 (block_pos / tok_pos, the two
+    ``index_put_``, ``attn_lens = old_lens + 1``, ``page16_decode_attention``).
+    """
+    q, block_table, cache_seqlens, batch, num_q_heads, num_kv_heads, head_dim, dev = _prepare(
+        q, k_cache, v_cache, block_table, cache_seqlens)
+    if k_new.dim() == 4:
+        k_new, v_new = k_new[:, 0], v_new[:, 0]
+    if tuple(k_new.shape) != (batch, num_kv_heads, head_dim) or tuple(v_new.shape) != tuple(k_new.shape):
+        raise RuntimeError("page16_native_shape_unsupported:new_token")
+    if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+        raise RuntimeError("page16_native_shape_unsupported:dtype")
+    if k_new.device != dev or v_new.device != dev:
+        raise RuntimeError("page16_native_unavailable:device")
+    if k_new.stride(2) != 1 or v_new.stride(2) != 1 or k_new.stride()[:2] != v_new.stride()[:2]:
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    out = torch.empty_like(q)
+    max_blocks = int(block_table.shape[1])
+    num_pages = min(int(k_cache.shape[0]), int(v_cache.shape[0]))
+
+    lib = _ext.load()
+    workspace = _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    code = lib.ukv_page16_decode_append(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_table.data_ptr(), cache_seqlens.data_ptr(),
+        k_new.data_ptr(), v_new.data_ptr(), _ext.i64_array(k_new.stride()[:2]), out.data_ptr(),
+        batch, num_q_heads, num_kv_heads, head_dim, int(n_rep),
+        max_blocks, num_pages,
+        _ext.i64_array(q.stride()[:2]),
+        _ext.i64_array(k_cache.stride()[:3]),
+        _ext.i64_array(v_cache.stride()[:3]),
+        float(softmax_scale), _DTYPE_CODES[q.dtype],
+        workspace.data_ptr(), workspace.numel(), stream,
+    )
+    if code != _ext.UKV_OK:
+        raise RuntimeError(_status_message(code, head_dim))
+    return out
+
+
+__all__ = ["HAS_TRITON", "HAS_UKV", "page16_decode_attention", "page16_decode_append_attention"]
