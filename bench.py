@@ -27,6 +27,8 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
   --workload step              a 32-layer decode step on the config-2 batch: prologue + fused
                                append/decode per layer, beside the unfused kernels and the
                                reference's call pattern (step_ragged: the config-3 batch)
+  --workload scores            config 5's importance scores computed: SnapKV observation-window
+                               block scores for 32 layers x 8 seqs at 32K (TFLOP/s vs MFMA peak)
   --workload prefill           config 4: chunked prefill, 4 x (16384 prefix + 2048 chunk),
                                TFLOP/s against the 2.5 PFLOP/s dense bf16 MFMA peak
 """
@@ -549,6 +551,81 @@ def run_compacted_decode(args, dev):
     return rec
 
 
+def run_scores(args, dev):
+    """Config 5's importance scores computed instead of given: SnapKV observation-window block
+    scores for 32 layers x 8 sequences at ctx 32768 (sink 64, obs 128), K read from the pool."""
+    import numpy as np
+    import torch
+
+    from oracle import snapkv_oracle
+    from unifiedkv_amd import compaction, snapkv
+    from unifiedkv_amd.pool import pack_block_table
+
+    pool, lists, _, k_blocks, _ = config5_pool(dev, args.seed, 0)
+    L, B, Hkv, D, obs, sink = C5["L"], C5["B"], C5["Hkv"], C5["D"], C5["obs"], C5["sink"]
+    Hq, ctx = 32, C5["ctx"]
+    table = torch.from_numpy(pack_block_table(lists)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 11)
+    q = torch.randn((B, L, Hq, obs, D), generator=g, device=dev).to(torch.bfloat16)
+
+    def step():
+        return snapkv.score_blocks(q, pool.k_cache, table, seq_len=ctx, sink_len=sink, obs_len=obs, n_rep=Hq // Hkv)
+
+    region_ms, per_ms = event_time_ms(step, args.steps, args.warmup)
+    kern_ms = sum(per_ms) / len(per_ms)
+    scores = step()
+    sel_ms, _ = event_time_ms(lambda: compaction.select_blocks(scores, k_blocks), args.steps, args.warmup)
+    aligned = snapkv.block_count(ctx, sink, obs) * 16
+    flops = B * L * 2 * (2 * Hq * obs * aligned * D)  # Q K^T in both passes
+    tflops = flops / (region_ms * 1e-3) / 1e12
+    log(f"[bench] scores: {region_ms * 1e3:.1f} us per call ({tflops:.1f} TFLOP/s), select {sel_ms * 1e3:.1f} us")
+    cpu = None
+    if not args.no_cpu_baseline:
+        # One KV head of one item (its 4 q heads x 128 queries over all 32576 mid keys), fp32 numpy.
+        ids = torch.tensor(lists[0], device=dev).long()
+        K = pool.k_cache[0].index_select(0, ids)[:, :, 0].reshape(-1, D)[sink:ctx - obs].float().cpu().numpy()
+        Qs = q[0, 0, : Hq // Hkv].float().cpu().numpy()
+        runs = []
+        t_end = time.perf_counter() + args.cpu_seconds
+        while time.perf_counter() < t_end or len(runs) < 2:
+            t0 = time.perf_counter()
+            snapkv_oracle.score_heads_f32(K, Qs, D ** -0.5)
+            runs.append(time.perf_counter() - t0)
+        med = sorted(runs)[len(runs) // 2]
+        f1 = 2 * (Hq // Hkv) * obs * K.shape[0] * D
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+        cpu = {"value": round(f1 / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": (f"dense fp32 observation-window scoring (numpy matmul, softmax, mean, max) of one KV "
+                          f"head's {Hq // Hkv} q heads x {obs} queries over {K.shape[0]} mid keys, median of "
+                          f"{len(runs)} runs (one pass; the GPU figure counts both passes' FLOPs)"),
+               "seconds_per_sample_run": round(med, 4)}
+    return {
+        "metric": "Config 5 SnapKV block scores (32 layers x 8 seqs x 32K, obs 128), attention-score TFLOP/s",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(region_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool and observation queries; fragmented page lists)",
+        "config": {"workload": "snapkv_scores_config5", "layers": L, "batch": B, "ctx": ctx, "sink": sink,
+                   "obs": obs, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
+                   "blocks_per_item": aligned // 16},
+        "flops_per_step": flops,
+        "select_us": round(sel_ms * 1e3, 1),
+        "roofline": {"bound": "mfma", "achieved": round(flops / (kern_ms * 1e-3) / 1e12, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flops / (kern_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel_us": round(kern_ms * 1e3, 1)},
+        "cpu_baseline": cpu,
+    }
+
+
 # ---------------------------------------------------------------------------------- config 4
 C4 = dict(B=4, prefix=16384, chunk=2048, Hq=32, Hkv=8, D=128)
 
@@ -659,7 +736,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill",
-                             "step", "step_ragged"])
+                             "step", "step_ragged", "scores"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -704,6 +781,8 @@ def main():
         rec = run_prefill(args, dev)
     elif args.workload in ("step", "step_ragged"):
         rec = run_step(args, dev)
+    elif args.workload == "scores":
+        rec = run_scores(args, dev)
     else:
         rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)

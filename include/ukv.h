@@ -21,6 +21,8 @@
  *                          core/scheduler.py:1092-1160 per-layer table / cache_seqlens build,
  *                          core/scheduler.py:1247-1265 commit (seq_len += 1)
  *   ukv_select_topk        core/scheduler.py:613-616, core/compress.py:141-142 block top-k + sort
+ *   ukv_snapkv_scores      core/scheduler.py:565-592 _score_layer_blocks_for_selection
+ *                          (core/compress.py:116-130): observation-window block importance
  *   ukv_kv_write_varlen    core/pool.py:127-141 for a prefill chunk appended after its prefix
  *   ukv_paged_prefill      core/engine.py:1826-1854 chunked prefill attention over past KV
  *                          (HF attention / core/varlen.py:19-42 flash_attn_varlen_func, causal)
@@ -218,6 +220,37 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
                       int max_chunk, int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks,
                       int num_pages, const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
                       float softmax_scale, int dtype, ukv_stream_t stream);
+
+/*
+ * SnapKV observation-window block scores (the importance scores ukv_select_topk ranks).
+ * For every item (layer l of sequence b, item = b * layers + l), with L = seq_len:
+ *   K_mid = K[:, sink_len : L - obs_len, :] zero-padded to aligned = ceil(L_mid / block_size)
+ *           * block_size keys;  A = softmax(Q_obs . repeat_kv(K_mid)^T * softmax_scale) over keys;
+ *   s = A.mean(over the obs_len queries).max(over the num_q_heads heads);
+ *   raw[n] = sum of s over keys [block_size * n, block_size * (n + 1));
+ *   scores[item * scores_stride + n] = max(raw[n-1], raw[n], raw[n+1]) if N >= 3, else raw[n]
+ * for n < N = ukv_snapkv_block_count(...), which is 0 (nothing written, UKV_OK) when
+ * L < sink_len + obs_len + block_size. fp32 arithmetic from 16-bit inputs.
+ *   q_obs        [items, num_q_heads, obs_len, head_dim], element strides q_strides[0..2]
+ *                {item, head, query}, last dimension contiguous
+ *   k            K rows with element strides k_strides[0..3] = {layer, seq-or-page, token, head}:
+ *                block_table NULL: token t of (b, l), head g at k + l*s0 + b*s1 + t*s2 + g*s3
+ *                (dense [layers][seqs][L][H_kv][D] or any strided view);
+ *                block_table [seqs, max_blocks] int32: page block_table[b][t / 16], slot t % 16 at
+ *                k + l*s0 + page*s1 + slot*s2 + g*s3 (the pool [layers, N, 16, H_kv, D]); page ids
+ *                outside [0, num_pages) read as zero rows
+ * num_q_heads must equal num_kv_heads * n_rep (q head h reads KV head h / n_rep). The workspace
+ * (ukv_snapkv_workspace_bytes) needs no initialisation. Replaces core/scheduler.py:565-592 and the
+ * scoring steps of core/compress.py:116-130.
+ */
+int ukv_snapkv_block_count(int seq_len, int sink_len, int obs_len, int block_size);
+size_t ukv_snapkv_workspace_bytes(int layers, int seqs, int seq_len, int sink_len, int obs_len, int num_q_heads,
+                                  int num_kv_heads, int head_dim, int n_rep, int block_size);
+int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                      const int32_t* block_table, int max_blocks, int num_pages, int layers, int seqs, int seq_len,
+                      int sink_len, int obs_len, int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                      int block_size, float softmax_scale, int dtype, float* scores, int64_t scores_stride,
+                      void* workspace, size_t workspace_bytes, ukv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@ SOURCES = [
     "page_ops.hip",
     "select.hip",
     "paged_prefill.hip",
+    "snapkv_score.hip",
 ]
 
 # Packed-FP32 VALU instructions are disabled for all device code.

@@ -115,6 +115,20 @@ SIGNATURES = {
             ctypes.c_float, _c_int, _c_void_p,  # scale dtype stream
         ],
     ),
+    "ukv_snapkv_block_count": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "ukv_snapkv_workspace_bytes": (
+        ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ukv_snapkv_scores": (
+        _c_int,
+        [
+            _c_void_p, _c_i64p, _c_void_p, _c_i64p,  # q_obs, strides, k, strides
+            _c_void_p, _c_int, _c_int,  # block_table, max_blocks, num_pages
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # layers, seqs, seq_len, sink, obs
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # Hq, Hkv, D, n_rep, block_size
+            ctypes.c_float, _c_int, _c_void_p, ctypes.c_int64,  # scale, dtype, scores, stride
+            _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
+        ],
+    ),
     "ukv_select_topk": (
         _c_int,
         [_c_void_p, ctypes.c_int64, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_void_p, ctypes.c_int64,

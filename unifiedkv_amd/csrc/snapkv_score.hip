@@ -1,0 +1,550 @@
+// SnapKV observation-window block scores for gfx950 (MI355X).
+//
+// For every item (one layer of one sequence) this computes what
+// core/scheduler.py:565-592 (_score_layer_blocks_for_selection) computes:
+//   K_mid = K[:, sink : L - obs, :], zero-padded to a multiple of the block size
+//   A     = softmax(Q_obs . repeat_kv(K_mid)^T * scale)      [H_q, obs, aligned]
+//   s     = A.mean(over obs queries).max(over q heads)       [aligned]
+//   block = s.view(N, block).sum(-1);  maxpool1d(k=3, s=1, p=1) when N >= 3
+// in fp32 from 16-bit Q and K (the reference runs these steps in the model
+// dtype; here every intermediate is fp32).
+//
+// Work decomposition: an item's mid keys form Kt tiles of 64 keys, split into
+// S contiguous ranges; one workgroup (8 waves) per (range, item). A unit is
+// one KV group's q heads, or part of them when n_rep * obs > 512 rows: the
+// unit's Q rows (up to 512 = 8 waves x 4 tiles of 16) stay in registers while
+// its K tiles stream through LDS (64 keys, 16-byte rows loaded once per
+// workgroup, padded pitch against bank conflicts). S = Q K^T runs on
+// v_mfma_f32_16x16x32 (A = 16 query rows, B = 16 keys: lane l holds query rows
+// 4*(l/16)+r of key l%16).
+//   pass 1 (stats): per query row, running max and sum of exp2 over the
+//           range's keys -> partial (m, l) per (range, row); a small kernel
+//           merges the ranges into (m, 1/l);
+//   pass 2 (scores): p = exp2(s - m) / l, summed over each head's queries
+//           (per-lane, then across the 4 lane groups, then the head's row tiles
+//           in a fixed order through LDS, so results are reproducible), max
+//           over heads, running max over units per key in LDS, then the sums
+//           over 16-key blocks of the range;
+//   finish: the 3-wide max pool over each item's blocks.
+// Both passes compute Q K^T, so the cost is 2 * (2 * H_q * obs * aligned * D)
+// FLOPs per item on the matrix cores; K is read twice.
+//
+// A scalar path (one thread per query row, plain loops) serves shapes the
+// tiled kernel is not instantiated for (head_dim not 64/128, obs not a
+// multiple of 16 or above 512, rows not 16-byte aligned).
+#include <algorithm>
+#include <cmath>
+
+#include "ukv_common.h"
+
+namespace ukv {
+
+constexpr int kSnapWaves = 8;
+constexpr int kSnapTile = 64;      // keys per LDS tile
+constexpr int kSnapMaxTW = 4;      // row tiles of 16 per wave -> at most 512 rows per unit
+constexpr int kSnapMaxKeys = 8192; // keys per range (LDS running max)
+
+struct SnapArgs {
+  const uint16_t* q;  // [items][H_q][obs][D] with strides q_si, q_sh, q_st
+  int64_t q_si, q_sh, q_st;
+  const uint16_t* k;  // token t, head g of item (b, l): see key_row()
+  int64_t k_sl, k_sb, k_st, k_sh;
+  const int32_t* table;  // [seqs][max_blocks] or null (dense)
+  int max_blocks, num_pages, page_size;
+  int layers, items;
+  int sink, obs, L_mid, aligned, n_blocks;
+  int Hq, Hkv, n_rep, D;
+  int hp, parts;         // q heads per unit, units per KV group
+  int S, Kt;             // key ranges per item, 64-key tiles per item
+  float scale_log2;
+  float2* part_stats;    // [items][S][Hq*obs] (m, l) per range
+  float2* stats;         // [items][Hq*obs] (m, 1/l)
+  float* raw;            // [items][n_blocks] block sums before pooling
+  float* out;            // [items][out_stride]
+  int64_t out_stride;
+};
+
+// Element offset of the K row of mid key j (token sink + j), head g, item
+// (b = item / layers, l = item % layers); -1 for a zero row (padding or an
+// invalid page id).
+__device__ __forceinline__ int64_t key_row(const SnapArgs& a, int item, int j, int g) {
+  if (j >= a.L_mid) return -1;
+  const int b = item / a.layers, l = item % a.layers;
+  const int t = a.sink + j;
+  int64_t off = (int64_t)l * a.k_sl + (int64_t)g * a.k_sh;
+  if (a.table) {
+    const int blk = t / a.page_size;
+    if (blk >= a.max_blocks) return -1;
+    const int page = a.table[(int64_t)b * a.max_blocks + blk];
+    if ((unsigned)page >= (unsigned)a.num_pages) return -1;
+    off += (int64_t)page * a.k_sb + (int64_t)(t % a.page_size) * a.k_st;
+  } else {
+    off += (int64_t)b * a.k_sb + (int64_t)t * a.k_st;
+  }
+  return off;
+}
+
+template <int D> struct SnapLds {
+  static constexpr int kPitch = D + 16;  // elements per key row in LDS
+  uint16_t kt[kSnapTile * kPitch];
+  float colpart[32][kSnapTile];          // per row tile of the unit (<= 32): column sums
+  float colmax[kSnapMaxKeys];            // running max over units, per key of the range
+  float red[kSnapWaves];
+};
+
+// TW: row tiles of 16 per wave (1, 2 or 4), the smallest that covers the unit.
+template <int DT, int D, bool SCORES, int TW>
+__global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapArgs a) {
+  constexpr int STEPS = D / 32;
+  constexpr int CHUNKS = kSnapTile * D / 8;  // 16-byte chunks per K tile
+  constexpr int CPT = CHUNKS / (64 * kSnapWaves);
+  static_assert(CHUNKS % (64 * kSnapWaves) == 0, "tile chunks must divide over the threads");
+  __shared__ SnapLds<D> lds;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int s = blockIdx.x, item = blockIdx.y;
+  const int t0 = (int)((int64_t)s * a.Kt / a.S), t1 = (int)((int64_t)(s + 1) * a.Kt / a.S);
+  const int key0 = t0 * kSnapTile;
+  const int R = a.hp * a.obs;                   // rows of a unit
+  const int T = R / 16;                         // row tiles of a unit
+  const int rows_all = a.Hq * a.obs;
+
+  if constexpr (SCORES) {
+    for (int i = tid; i < (t1 - t0) * kSnapTile; i += blockDim.x) lds.colmax[i] = 0.f;
+  }
+
+  for (int u = 0; u < a.Hkv * a.parts; ++u) {
+    const int g = u / a.parts;
+    const int h0 = g * a.n_rep + (u % a.parts) * a.hp;  // first q head of the unit
+
+    // This wave's row tiles: w*TW .. w*TW+TW-1 (rows beyond R are zero).
+    u32x4 qa[TW][STEPS];
+    float m[TW][4], lsum[TW][4];
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+      const int tile = wv * TW + k;
+      const bool on = tile < T;
+      const int rr = tile * 16 + l16;  // A row of this lane
+      const uint16_t* qp = a.q + (int64_t)item * a.q_si + (int64_t)(h0 + rr / a.obs) * a.q_sh +
+                           (int64_t)(rr % a.obs) * a.q_st + 8 * lg;
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) qa[k][st] = on ? ld16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        m[k][r] = -INFINITY;
+        lsum[k][r] = 0.f;
+        if constexpr (SCORES) {
+          if (on) {  // C rows 4*lg + r of the tile
+            const int row = tile * 16 + 4 * lg + r;
+            const float2 st2 = a.stats[(int64_t)item * rows_all + (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs];
+            m[k][r] = st2.x;
+            lsum[k][r] = st2.y;  // 1/l
+          }
+        }
+      }
+    }
+
+    // K tile load: thread chunk c = tid + i*512 -> key c / (D/8), dims 8*(c % (D/8)).
+    u32x4 pre[CPT];
+    auto fetch = [&](int tile_idx) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * 64 * kSnapWaves;
+        const int key = tile_idx * kSnapTile + c / (D / 8);
+        const int64_t off = key_row(a, item, key, g);
+        pre[i] = off >= 0 ? ld16(a.k + off + 8 * (c % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    for (int ti = t0; ti < t1; ++ti) {
+      fetch(ti);
+      __syncthreads();  // previous tile's LDS reads (and colsum use) are done
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * 64 * kSnapWaves;
+        *reinterpret_cast<u32x4*>(&lds.kt[(c / (D / 8)) * SnapLds<D>::kPitch + 8 * (c % (D / 8))]) = pre[i];
+      }
+      __syncthreads();
+
+      const int kbase = ti * kSnapTile;
+      // S tiles: column tile ct (16 keys) at a time, its B operands (key l16,
+      // dims 8*lg + 32*st) read from LDS once and used by every row tile.
+      f32x4 acc[TW][4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        u32x4 kb[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st)
+          kb[st] = *reinterpret_cast<const u32x4*>(&lds.kt[(ct * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
+#pragma unroll
+        for (int k = 0; k < TW; ++k) {  // tiles past T hold zero Q rows
+          acc[k][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int st = 0; st < STEPS; ++st) acc[k][ct] = mfma16x16x32<DT>(qa[k][st], kb[st], acc[k][ct]);
+        }
+      }
+      // Keys at or past the padded end are masked.
+      bool kvalid[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) kvalid[ct] = kbase + ct * 16 + l16 < a.aligned;
+
+#pragma unroll
+      for (int k = 0; k < TW; ++k) {
+        const int tile = wv * TW + k;
+        if (tile >= T) break;  // wave-uniform
+        float sc[4][4];                   // [column tile][row r], log2 units
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[ct][r] = kvalid[ct] ? acc[k][ct][r] * a.scale_log2 : -INFINITY;
+        if constexpr (!SCORES) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float tmax = fmaxf(fmaxf(sc[0][r], sc[1][r]), fmaxf(sc[2][r], sc[3][r]));
+            tmax = row_max16(tmax);
+            const float mn = fmaxf(m[k][r], tmax);
+            float e = 0.f;
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) e += fast_exp2(sc[ct][r] - mn);
+            e = row_sum16(e);
+            lsum[k][r] = lsum[k][r] * fast_exp2(m[k][r] - mn) + e;
+            m[k][r] = mn;
+          }
+        } else {
+          // Column sums over the tile's 16 query rows (one head: obs % 16 == 0).
+          float v[4];
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct) {
+            float x = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x += fast_exp2(sc[ct][r] - m[k][r]) * lsum[k][r];
+            x += __shfl_xor(x, 16);
+            x += __shfl_xor(x, 32);
+            v[ct] = x;
+          }
+          // Key `lane` of this tile; summed per head below in a fixed order.
+          lds.colpart[tile][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
+        }
+      }
+      if constexpr (SCORES) {
+        __syncthreads();
+        if (tid < kSnapTile) {
+          const int tph = a.obs / 16;  // row tiles per head
+          float mx = 0.f;
+          for (int h = 0; h < a.hp; ++h) {
+            float x = 0.f;
+            for (int q = 0; q < tph; ++q) x += lds.colpart[h * tph + q][tid];
+            mx = fmaxf(mx, x);
+          }
+          const int j = kbase + tid - key0;
+          lds.colmax[j] = fmaxf(lds.colmax[j], mx);
+        }
+      }
+    }
+
+    if constexpr (!SCORES) {
+      // Partial (m, l) of this range for the unit's rows.
+#pragma unroll
+      for (int k = 0; k < TW; ++k) {
+        const int tile = wv * TW + k;
+        if (tile >= T) break;
+        if (l16 == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = tile * 16 + 4 * lg + r;
+            const int64_t grow = (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs;
+            a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(m[k][r], lsum[k][r]);
+          }
+        }
+      }
+    }
+  }
+
+  if constexpr (SCORES) {
+    __syncthreads();
+    // Sums over 16-key blocks of the range, divided by obs (the mean over queries).
+    const float inv_obs = 1.f / (float)a.obs;
+    const int nb = (t1 - t0) * (kSnapTile / 16);
+    for (int i = tid; i < nb; i += blockDim.x) {
+      const int n = key0 / 16 + i;
+      if (n >= a.n_blocks) continue;
+      float x = 0.f;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) x += lds.colmax[16 * i + t];
+      a.raw[(int64_t)item * a.n_blocks + n] = x * inv_obs;
+    }
+  }
+}
+
+// (m, l) partials of the S ranges -> (m, 1/l) per (item, row).
+__global__ void __launch_bounds__(256) snap_stats_merge_kernel(const SnapArgs a) {
+  const int rows_all = a.Hq * a.obs;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.items * rows_all) return;
+  const int64_t item = idx / rows_all, row = idx % rows_all;
+  float mx = -INFINITY;
+  for (int s = 0; s < a.S; ++s) mx = fmaxf(mx, a.part_stats[(item * a.S + s) * rows_all + row].x);
+  float l = 0.f;
+  for (int s = 0; s < a.S; ++s) {
+    const float2 p = a.part_stats[(item * a.S + s) * rows_all + row];
+    l += p.y * fast_exp2(p.x - mx);
+  }
+  a.stats[idx] = make_float2(mx, 1.f / l);
+}
+
+// out[item][n] = max(raw[n-1], raw[n], raw[n+1]) when n_blocks >= 3, else raw[n].
+__global__ void __launch_bounds__(256) snap_pool_kernel(const SnapArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.items * a.n_blocks) return;
+  const int64_t item = idx / a.n_blocks;
+  const int n = (int)(idx % a.n_blocks);
+  const float* r = a.raw + item * a.n_blocks;
+  float x = r[n];
+  if (a.n_blocks >= 3) {
+    if (n > 0) x = fmaxf(x, r[n - 1]);
+    if (n + 1 < a.n_blocks) x = fmaxf(x, r[n + 1]);
+  }
+  a.out[item * a.out_stride + n] = x;
+}
+
+// Scalar path, pass 1: one thread per (item, q head, query): (m, 1/l) over all keys.
+template <int DT>
+__global__ void __launch_bounds__(256) snap_scalar_stats_kernel(const SnapArgs a) {
+  const int rows_all = a.Hq * a.obs;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.items * rows_all) return;
+  const int item = (int)(idx / rows_all), row = (int)(idx % rows_all);
+  const int h = row / a.obs, i = row % a.obs, g = h / a.n_rep;
+  const uint16_t* qp = a.q + (int64_t)item * a.q_si + (int64_t)h * a.q_sh + (int64_t)i * a.q_st;
+  float mx = -INFINITY, l = 0.f;
+  for (int j = 0; j < a.aligned; ++j) {
+    const int64_t off = key_row(a, item, j, g);
+    float dot = 0.f;
+    if (off >= 0)
+      for (int d = 0; d < a.D; ++d) dot += Elem<DT>::one(qp[d]) * Elem<DT>::one(a.k[off + d]);
+    const float x = dot * a.scale_log2;
+    const float mn = fmaxf(mx, x);
+    l = l * fast_exp2(mx - mn) + fast_exp2(x - mn);
+    mx = mn;
+  }
+  a.stats[idx] = make_float2(mx, 1.f / l);
+}
+
+// Scalar path, pass 2: one workgroup per (item, 16-key block): thread t < 16
+// owns key 16n + t and loops over every (head, query).
+template <int DT>
+__global__ void __launch_bounds__(64) snap_scalar_scores_kernel(const SnapArgs a) {
+  const int item = blockIdx.y, n = blockIdx.x;
+  __shared__ float col[16];
+  const int t = threadIdx.x;
+  if (t < 16) {
+    const int j = 16 * n + t;
+    float best = 0.f;
+    for (int h = 0; h < a.Hq; ++h) {
+      const int g = h / a.n_rep;
+      const int64_t off = key_row(a, item, j, g);
+      float sum = 0.f;
+      for (int i = 0; i < a.obs; ++i) {
+        const uint16_t* qp = a.q + (int64_t)item * a.q_si + (int64_t)h * a.q_sh + (int64_t)i * a.q_st;
+        float dot = 0.f;
+        if (off >= 0)
+          for (int d = 0; d < a.D; ++d) dot += Elem<DT>::one(qp[d]) * Elem<DT>::one(a.k[off + d]);
+        const float2 st = a.stats[(int64_t)item * a.Hq * a.obs + (int64_t)h * a.obs + i];
+        sum += fast_exp2(dot * a.scale_log2 - st.x) * st.y;
+      }
+      best = fmaxf(best, sum / (float)a.obs);
+    }
+    col[t] = best;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float x = 0.f;
+    for (int u = 0; u < 16; ++u) x += col[u];
+    a.raw[(int64_t)item * a.n_blocks + n] = x;
+  }
+}
+
+namespace {
+
+int snap_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  return cus;
+}
+
+size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct SnapPlan {
+  bool tiled;
+  int hp, parts, S, Kt, aligned, n_blocks, L_mid;
+  size_t part_off, stats_off, raw_off, total;
+};
+
+SnapPlan snap_plan(int items, int seq_len, int sink, int obs, int num_q_heads, int n_rep, int head_dim,
+                   int block_size, bool aligned_rows) {
+  SnapPlan p{};
+  p.L_mid = seq_len - sink - obs;
+  p.aligned = ((std::max(1, p.L_mid) + block_size - 1) / block_size) * block_size;
+  p.n_blocks = p.aligned / block_size;
+  p.Kt = (p.aligned + kSnapTile - 1) / kSnapTile;
+  // Heads per unit: the largest divisor of n_rep whose rows fit 8 waves x 4 tiles.
+  p.hp = 0;
+  for (int h = std::min(n_rep, 32); h >= 1; --h)
+    if (n_rep % h == 0 && h * obs <= 16 * kSnapWaves * kSnapMaxTW) {
+      p.hp = h;
+      break;
+    }
+  p.tiled = (head_dim == 64 || head_dim == 128) && obs % 16 == 0 && p.hp > 0 && aligned_rows && block_size == 16;
+  p.parts = p.tiled ? n_rep / p.hp : 1;
+  if (p.tiled) {
+    const int want = (2 * snap_cu_count() + items - 1) / std::max(1, items);
+    const int need = (p.Kt * kSnapTile + kSnapMaxKeys - 1) / kSnapMaxKeys;
+    p.S = std::max(need, std::min(want, std::max(1, p.Kt / 4)));
+    p.S = std::min(p.S, p.Kt);
+  } else {
+    p.S = 1;
+  }
+  const size_t rows_all = (size_t)num_q_heads * obs;
+  p.part_off = 0;
+  p.stats_off = a256((size_t)items * p.S * rows_all * sizeof(float2));
+  p.raw_off = p.stats_off + a256((size_t)items * rows_all * sizeof(float2));
+  p.total = p.raw_off + a256((size_t)items * p.n_blocks * sizeof(float));
+  return p;
+}
+
+template <int DT, int D, int TW>
+void launch_tiled(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
+  const int64_t rows = (int64_t)a.items * a.Hq * a.obs;
+  const dim3 grid(p.S, a.items);
+  hipLaunchKernelGGL((snap_tile_kernel<DT, D, false, TW>), grid, dim3(64 * kSnapWaves), 0, st, a);
+  hipLaunchKernelGGL(snap_stats_merge_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((snap_tile_kernel<DT, D, true, TW>), grid, dim3(64 * kSnapWaves), 0, st, a);
+}
+
+template <int DT, int D>
+void launch_tiled_tw(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
+  const int T = a.hp * a.obs / 16;
+  if (T <= kSnapWaves)
+    launch_tiled<DT, D, 1>(a, p, st);
+  else if (T <= 2 * kSnapWaves)
+    launch_tiled<DT, D, 2>(a, p, st);
+  else
+    launch_tiled<DT, D, 4>(a, p, st);
+}
+
+template <int DT>
+void launch_snap(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
+  if (p.tiled) {
+    if (a.D == 64)
+      launch_tiled_tw<DT, 64>(a, p, st);
+    else
+      launch_tiled_tw<DT, 128>(a, p, st);
+  } else {
+    const int64_t rows = (int64_t)a.items * a.Hq * a.obs;
+    hipLaunchKernelGGL(snap_scalar_stats_kernel<DT>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(snap_scalar_scores_kernel<DT>, dim3(a.n_blocks, a.items), dim3(64), 0, st, a);
+  }
+  const int64_t nout = (int64_t)a.items * a.n_blocks;
+  hipLaunchKernelGGL(snap_pool_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, st, a);
+}
+
+bool snap_aligned(const void* q, const void* k, const int64_t* qs, const int64_t* ks) {
+  auto m8 = [](int64_t x) { return (x & 7) == 0; };
+  return (reinterpret_cast<uintptr_t>(q) & 15u) == 0 && (reinterpret_cast<uintptr_t>(k) & 15u) == 0 && m8(qs[0]) &&
+         m8(qs[1]) && m8(qs[2]) && m8(ks[0]) && m8(ks[1]) && m8(ks[2]) && m8(ks[3]);
+}
+
+bool snap_shape_ok(int layers, int seqs, int seq_len, int sink, int obs, int num_q_heads, int num_kv_heads,
+                   int head_dim, int n_rep, int block_size) {
+  return layers > 0 && seqs > 0 && seq_len > 0 && sink >= 0 && obs > 0 && num_q_heads > 0 && num_kv_heads > 0 &&
+         head_dim > 0 && n_rep > 0 && block_size > 0 && num_q_heads == num_kv_heads * n_rep;
+}
+
+}  // namespace
+}  // namespace ukv
+
+using namespace ukv;
+
+extern "C" int ukv_snapkv_block_count(int seq_len, int sink_len, int obs_len, int block_size) {
+  if (block_size <= 0 || seq_len < sink_len + obs_len + block_size) return 0;
+  const int L_mid = seq_len - sink_len - obs_len;
+  return (std::max(1, L_mid) + block_size - 1) / block_size;
+}
+
+extern "C" size_t ukv_snapkv_workspace_bytes(int layers, int seqs, int seq_len, int sink_len, int obs_len,
+                                             int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                                             int block_size) {
+  if (!snap_shape_ok(layers, seqs, seq_len, sink_len, obs_len, num_q_heads, num_kv_heads, head_dim, n_rep,
+                     block_size) ||
+      ukv_snapkv_block_count(seq_len, sink_len, obs_len, block_size) == 0)
+    return 0;
+  // The tiled plan needs at least as much as the scalar one; size for the larger.
+  return snap_plan(layers * seqs, seq_len, sink_len, obs_len, num_q_heads, n_rep, head_dim, block_size, true).total;
+}
+
+extern "C" int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                 const int32_t* block_table, int max_blocks, int num_pages, int layers, int seqs,
+                                 int seq_len, int sink_len, int obs_len, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int n_rep, int block_size, float softmax_scale, int dtype,
+                                 float* scores, int64_t scores_stride, void* workspace, size_t workspace_bytes,
+                                 ukv_stream_t stream) {
+  if (!snap_shape_ok(layers, seqs, seq_len, sink_len, obs_len, num_q_heads, num_kv_heads, head_dim, n_rep,
+                     block_size))
+    return UKV_ERR_INVALID_ARGUMENT;
+  if (dtype != UKV_DTYPE_F16 && dtype != UKV_DTYPE_BF16) return UKV_ERR_DTYPE;
+  const int n_blocks = ukv_snapkv_block_count(seq_len, sink_len, obs_len, block_size);
+  if (n_blocks == 0) return UKV_OK;  // too short: no middle blocks to score (the reference's empty result)
+  if (!q_obs || !q_strides || !k || !k_strides || !scores || scores_stride < n_blocks) return UKV_ERR_INVALID_ARGUMENT;
+  if (block_table && (max_blocks <= 0 || num_pages <= 0)) return UKV_ERR_INVALID_ARGUMENT;
+  if ((int64_t)layers * seqs > 65535) return UKV_ERR_INVALID_ARGUMENT;
+  const int items = layers * seqs;
+  const SnapPlan p = snap_plan(items, seq_len, sink_len, obs_len, num_q_heads, n_rep, head_dim, block_size,
+                               snap_aligned(q_obs, k, q_strides, k_strides));
+  if (!workspace || workspace_bytes < p.total || (reinterpret_cast<uintptr_t>(workspace) & 15u)) return UKV_ERR_WORKSPACE;
+
+  SnapArgs a{};
+  a.q = static_cast<const uint16_t*>(q_obs);
+  a.q_si = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.q_st = q_strides[2];
+  a.k = static_cast<const uint16_t*>(k);
+  a.k_sl = k_strides[0];
+  a.k_sb = k_strides[1];
+  a.k_st = k_strides[2];
+  a.k_sh = k_strides[3];
+  a.table = block_table;
+  a.max_blocks = max_blocks;
+  a.num_pages = num_pages;
+  a.page_size = 16;
+  a.layers = layers;
+  a.items = items;
+  a.sink = sink_len;
+  a.obs = obs_len;
+  a.L_mid = p.L_mid;
+  a.aligned = p.aligned;
+  a.n_blocks = p.n_blocks;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.n_rep = n_rep;
+  a.D = head_dim;
+  a.hp = p.hp;
+  a.parts = p.parts;
+  a.S = p.S;
+  a.Kt = p.Kt;
+  a.scale_log2 = softmax_scale * kLog2e;
+  char* ws = static_cast<char*>(workspace);
+  a.part_stats = reinterpret_cast<float2*>(ws + p.part_off);
+  a.stats = reinterpret_cast<float2*>(ws + p.stats_off);
+  a.raw = reinterpret_cast<float*>(ws + p.raw_off);
+  a.out = scores;
+  a.out_stride = scores_stride;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == UKV_DTYPE_BF16)
+    launch_snap<UKV_DTYPE_BF16>(a, p, st);
+  else
+    launch_snap<UKV_DTYPE_F16>(a, p, st);
+  return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
+}
