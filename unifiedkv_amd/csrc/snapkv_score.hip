@@ -58,7 +58,7 @@ struct SnapArgs {
   int S, Kt;             // key ranges per item, 64-key tiles per item
   float scale_log2;
   float2* part_stats;    // [items][S][Hq*obs] (m, l) per range
-  float2* stats;         // [items][Hq*obs] (m, 1/l)
+  float2* stats;         // [items][Hq*obs] (m + log2(l), unused)
   float* raw;            // [items][n_blocks] block sums before pooling
   float* out;            // [items][out_stride]
   int64_t out_stride;
@@ -86,18 +86,29 @@ __device__ __forceinline__ int64_t key_row(const SnapArgs& a, int item, int j, i
 
 template <int D> struct SnapLds {
   static constexpr int kPitch = D + 16;  // elements per key row in LDS
-  uint16_t kt[kSnapTile * kPitch];
+  alignas(16) uint16_t kt[kSnapTile * kPitch];  // 16-byte aligned: ds_read_b128 / ds_write_b128
   float colpart[32][kSnapTile];          // per row tile of the unit (<= 32): column sums
   float colmax[kSnapMaxKeys];            // running max over units, per key of the range
   float red[kSnapWaves];
 };
 
 // TW: row tiles of 16 per wave (1, 2 or 4), the smallest that covers the unit.
+//
+// Lane l of a wave holds, for each of its row tiles k, query rows 4*(l/16) + r
+// (r < 4) of key column l%16 in each 16-key column tile ct.
+//   pass 1 keeps a running (max, sum) per lane and row over the lane's own keys:
+//          the max moves only when a wave-wide vote finds a score above it by
+//          more than 2^8 (weights stay <= 256), and the 16 lanes of a row are
+//          merged once per range, not per tile;
+//   pass 2 gets m' = m + log2(l) per row, so p = exp2(s * scale - m') is one
+//          FMA and one exp2; each lane adds its p over the rows of its tiles that
+//          belong to one head, and only then are the 4 lane groups summed.
 template <int DT, int D, bool SCORES, int TW>
 __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapArgs a) {
   constexpr int STEPS = D / 32;
   constexpr int CHUNKS = kSnapTile * D / 8;  // 16-byte chunks per K tile
   constexpr int CPT = CHUNKS / (64 * kSnapWaves);
+  constexpr float kTau = 8.f;
   static_assert(CHUNKS % (64 * kSnapWaves) == 0, "tile chunks must divide over the threads");
   __shared__ SnapLds<D> lds;
 
@@ -108,21 +119,22 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
   const int s = blockIdx.x, item = blockIdx.y;
   const int t0 = (int)((int64_t)s * a.Kt / a.S), t1 = (int)((int64_t)(s + 1) * a.Kt / a.S);
   const int key0 = t0 * kSnapTile;
-  const int R = a.hp * a.obs;                   // rows of a unit
-  const int T = R / 16;                         // row tiles of a unit
+  const int R = a.hp * a.obs;  // rows of a unit
+  const int T = R / 16;        // row tiles of a unit
+  const int tph = a.obs / 16;  // row tiles per q head
   const int rows_all = a.Hq * a.obs;
+  const float c = a.scale_log2;
 
-  if constexpr (SCORES) {
+  if constexpr (SCORES)
     for (int i = tid; i < (t1 - t0) * kSnapTile; i += blockDim.x) lds.colmax[i] = 0.f;
-  }
 
   for (int u = 0; u < a.Hkv * a.parts; ++u) {
     const int g = u / a.parts;
     const int h0 = g * a.n_rep + (u % a.parts) * a.hp;  // first q head of the unit
 
-    // This wave's row tiles: w*TW .. w*TW+TW-1 (rows beyond R are zero).
+    // This wave's row tiles: w*TW .. w*TW+TW-1 (tiles past T are zero and unused).
     u32x4 qa[TW][STEPS];
-    float m[TW][4], lsum[TW][4];
+    float m[TW][4], lsum[TW][4];  // pass 1: running max / sum; pass 2: m' = m + log2(l)
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
       const int tile = wv * TW + k;
@@ -139,38 +151,37 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
         if constexpr (SCORES) {
           if (on) {  // C rows 4*lg + r of the tile
             const int row = tile * 16 + 4 * lg + r;
-            const float2 st2 = a.stats[(int64_t)item * rows_all + (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs];
-            m[k][r] = st2.x;
-            lsum[k][r] = st2.y;  // 1/l
+            m[k][r] = a.stats[(int64_t)item * rows_all + (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs].x;
           }
         }
       }
     }
 
-    // K tile load: thread chunk c = tid + i*512 -> key c / (D/8), dims 8*(c % (D/8)).
+    // K tile loads: thread chunk cc = tid + i*512 -> key cc / (D/8), dims 8*(cc % (D/8)).
     u32x4 pre[CPT];
     auto fetch = [&](int tile_idx) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * 64 * kSnapWaves;
-        const int key = tile_idx * kSnapTile + c / (D / 8);
+        const int cc = tid + i * 64 * kSnapWaves;
+        const int key = tile_idx * kSnapTile + cc / (D / 8);
         const int64_t off = key_row(a, item, key, g);
-        pre[i] = off >= 0 ? ld16(a.k + off + 8 * (c % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
+        pre[i] = off >= 0 ? ld16(a.k + off + 8 * (cc % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
       }
     };
+    fetch(t0);
     for (int ti = t0; ti < t1; ++ti) {
-      fetch(ti);
-      __syncthreads();  // previous tile's LDS reads (and colsum use) are done
+      __syncthreads();  // every wave is done with the previous tile (and its colpart)
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * 64 * kSnapWaves;
-        *reinterpret_cast<u32x4*>(&lds.kt[(c / (D / 8)) * SnapLds<D>::kPitch + 8 * (c % (D / 8))]) = pre[i];
+        const int cc = tid + i * 64 * kSnapWaves;
+        *reinterpret_cast<u32x4*>(&lds.kt[(cc / (D / 8)) * SnapLds<D>::kPitch + 8 * (cc % (D / 8))]) = pre[i];
       }
       __syncthreads();
+      if (ti + 1 < t1) fetch(ti + 1);  // in flight while this tile is reduced
 
       const int kbase = ti * kSnapTile;
-      // S tiles: column tile ct (16 keys) at a time, its B operands (key l16,
-      // dims 8*lg + 32*st) read from LDS once and used by every row tile.
+      // S tiles, one 16-key column tile at a time: its B operands (key l16, dims
+      // 8*lg + 32*st) are read from LDS once and used by every row tile.
       f32x4 acc[TW][4];
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
@@ -179,63 +190,91 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
         for (int st = 0; st < STEPS; ++st)
           kb[st] = *reinterpret_cast<const u32x4*>(&lds.kt[(ct * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
 #pragma unroll
-        for (int k = 0; k < TW; ++k) {  // tiles past T hold zero Q rows
+        for (int k = 0; k < TW; ++k) {
           acc[k][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int st = 0; st < STEPS; ++st) acc[k][ct] = mfma16x16x32<DT>(qa[k][st], kb[st], acc[k][ct]);
         }
       }
-      // Keys at or past the padded end are masked.
-      bool kvalid[4];
+      // Keys at or past the padded end (only in the last tile of an item) are masked;
+      // a 16-key column tile is either wholly valid or wholly masked (aligned % 16 == 0).
+      const bool full = kbase + kSnapTile <= a.aligned;
+      bool cvalid[4];
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) kvalid[ct] = kbase + ct * 16 + l16 < a.aligned;
+      for (int ct = 0; ct < 4; ++ct) cvalid[ct] = full || kbase + 16 * ct < a.aligned;
 
+      if constexpr (!SCORES) {
+        // This lane's max over its valid keys of the tile, per row (column tile 0 is always valid).
+        auto tile_max = [&](int k, int r) {
+          float x = acc[k][0][r];
 #pragma unroll
-      for (int k = 0; k < TW; ++k) {
-        const int tile = wv * TW + k;
-        if (tile >= T) break;  // wave-uniform
-        float sc[4][4];                   // [column tile][row r], log2 units
+          for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[k][ct][r]) : x;
+          return x * c;
+        };
+        bool up = false;
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
+        for (int k = 0; k < TW; ++k)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[ct][r] = kvalid[ct] ? acc[k][ct][r] * a.scale_log2 : -INFINITY;
-        if constexpr (!SCORES) {
+          for (int r = 0; r < 4; ++r) up |= tile_max(k, r) > m[k][r] + kTau;
+        if (__any(up)) {
+#pragma unroll
+          for (int k = 0; k < TW; ++k)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float mn = fmaxf(m[k][r], tile_max(k, r));
+              lsum[k][r] *= fast_exp2(m[k][r] - mn);
+              m[k][r] = mn;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < TW; ++k)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float tmax = fmaxf(fmaxf(sc[0][r], sc[1][r]), fmaxf(sc[2][r], sc[3][r]));
-            tmax = row_max16(tmax);
-            const float mn = fmaxf(m[k][r], tmax);
             float e = 0.f;
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct) e += fast_exp2(sc[ct][r] - mn);
-            e = row_sum16(e);
-            lsum[k][r] = lsum[k][r] * fast_exp2(m[k][r] - mn) + e;
-            m[k][r] = mn;
+            for (int ct = 0; ct < 4; ++ct) {
+              const float p = fast_exp2(__builtin_fmaf(acc[k][ct][r], c, -m[k][r]));
+              e += cvalid[ct] ? p : 0.f;
+            }
+            lsum[k][r] += e;
           }
-        } else {
-          // Column sums over the tile's 16 query rows (one head: obs % 16 == 0).
-          float v[4];
+      } else {
+        // Column sums over the rows of each run of this wave's tiles that share a head.
+        float colacc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < TW; ++k) {
+          const int tile = wv * TW + k;
+          if (tile >= T) break;  // wave-uniform
 #pragma unroll
           for (int ct = 0; ct < 4; ++ct) {
             float x = 0.f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x += fast_exp2(sc[ct][r] - m[k][r]) * lsum[k][r];
-            x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            v[ct] = x;
+            for (int r = 0; r < 4; ++r) x += fast_exp2(__builtin_fmaf(acc[k][ct][r], c, -m[k][r]));
+            colacc[ct] += cvalid[ct] ? x : 0.f;
           }
-          // Key `lane` of this tile; summed per head below in a fixed order.
-          lds.colpart[tile][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
+          const bool last_of_run = k == TW - 1 || tile + 1 >= T || (tile + 1) % tph == 0;
+          if (last_of_run) {
+            float v[4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+              float x = colacc[ct];
+              x += __shfl_xor(x, 16);
+              x += __shfl_xor(x, 32);
+              v[ct] = x;
+              colacc[ct] = 0.f;
+            }
+            // The run's first tile holds the run's sums (key `lane` of this tile).
+            const int first = max(wv * TW, (tile / tph) * tph);
+            lds.colpart[first][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
+          }
         }
-      }
-      if constexpr (SCORES) {
         __syncthreads();
         if (tid < kSnapTile) {
-          const int tph = a.obs / 16;  // row tiles per head
           float mx = 0.f;
           for (int h = 0; h < a.hp; ++h) {
             float x = 0.f;
-            for (int q = 0; q < tph; ++q) x += lds.colpart[h * tph + q][tid];
+            for (int q = h * tph; q < (h + 1) * tph; ++q)
+              if (q == h * tph || q % TW == 0) x += lds.colpart[q][tid];  // run starts, fixed order
             mx = fmaxf(mx, x);
           }
           const int j = kbase + tid - key0;
@@ -245,17 +284,18 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
     }
 
     if constexpr (!SCORES) {
-      // Partial (m, l) of this range for the unit's rows.
+      // Merge the 16 lanes of each row, then write this range's partial (m, l).
 #pragma unroll
       for (int k = 0; k < TW; ++k) {
         const int tile = wv * TW + k;
-        if (tile >= T) break;
-        if (l16 == 0) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4; ++r) {
+          const float mm = row_max16(m[k][r]);
+          const float ll = row_sum16(lsum[k][r] * fast_exp2(m[k][r] - mm));
+          if (tile < T && l16 == 0) {
             const int row = tile * 16 + 4 * lg + r;
             const int64_t grow = (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs;
-            a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(m[k][r], lsum[k][r]);
+            a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(mm, ll);
           }
         }
       }
@@ -278,7 +318,8 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
   }
 }
 
-// (m, l) partials of the S ranges -> (m, 1/l) per (item, row).
+// (m, l) partials of the S ranges -> m' = m + log2(l) per (item, row), so that
+// the weight of a score x (log2 units) is exp2(x - m').
 __global__ void __launch_bounds__(256) snap_stats_merge_kernel(const SnapArgs a) {
   const int rows_all = a.Hq * a.obs;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -291,7 +332,7 @@ __global__ void __launch_bounds__(256) snap_stats_merge_kernel(const SnapArgs a)
     const float2 p = a.part_stats[(item * a.S + s) * rows_all + row];
     l += p.y * fast_exp2(p.x - mx);
   }
-  a.stats[idx] = make_float2(mx, 1.f / l);
+  a.stats[idx] = make_float2(mx + log2f(l), 0.f);
 }
 
 // out[item][n] = max(raw[n-1], raw[n], raw[n+1]) when n_blocks >= 3, else raw[n].
@@ -329,7 +370,7 @@ __global__ void __launch_bounds__(256) snap_scalar_stats_kernel(const SnapArgs a
     l = l * fast_exp2(mx - mn) + fast_exp2(x - mn);
     mx = mn;
   }
-  a.stats[idx] = make_float2(mx, 1.f / l);
+  a.stats[idx] = make_float2(mx + log2f(l), 0.f);
 }
 
 // Scalar path, pass 2: one workgroup per (item, 16-key block): thread t < 16
@@ -352,7 +393,7 @@ __global__ void __launch_bounds__(64) snap_scalar_scores_kernel(const SnapArgs a
         if (off >= 0)
           for (int d = 0; d < a.D; ++d) dot += Elem<DT>::one(qp[d]) * Elem<DT>::one(a.k[off + d]);
         const float2 st = a.stats[(int64_t)item * a.Hq * a.obs + (int64_t)h * a.obs + i];
-        sum += fast_exp2(dot * a.scale_log2 - st.x) * st.y;
+        sum += fast_exp2(dot * a.scale_log2 - st.x);
       }
       best = fmaxf(best, sum / (float)a.obs);
     }
