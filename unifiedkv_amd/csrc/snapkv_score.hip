@@ -34,6 +34,7 @@
 // multiple of 16 or above 512, rows not 16-byte aligned).
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "ukv_common.h"
 
@@ -86,10 +87,9 @@ __device__ __forceinline__ int64_t key_row(const SnapArgs& a, int item, int j, i
 
 template <int D> struct SnapLds {
   static constexpr int kPitch = D + 16;  // elements per key row in LDS
-  alignas(16) uint16_t kt[kSnapTile * kPitch];  // 16-byte aligned: ds_read_b128 / ds_write_b128
-  float colpart[32][kSnapTile];          // per row tile of the unit (<= 32): column sums
+  alignas(16) uint16_t kt[2][kSnapTile * kPitch];  // double-buffered K tiles (ds_read_b128 / ds_write_b128)
+  float colpart[2][32][kSnapTile];       // double-buffered column sums per run of row tiles (<= 32 tiles)
   float colmax[kSnapMaxKeys];            // running max over units, per key of the range
-  float red[kSnapWaves];
 };
 
 // TW: row tiles of 16 per wave (1, 2 or 4), the smallest that covers the unit.
@@ -102,7 +102,9 @@ template <int D> struct SnapLds {
 //          merged once per range, not per tile;
 //   pass 2 gets m' = m + log2(l) per row, so p = exp2(s * scale - m') is one
 //          FMA and one exp2; each lane adds its p over the rows of its tiles that
-//          belong to one head, and only then are the 4 lane groups summed.
+//          belong to one head, then the 4 lane groups are summed; the runs of a
+//          head are added and the max over heads taken by 64 * hp threads.
+// K tiles and column sums are double-buffered: one barrier per tile.
 template <int DT, int D, bool SCORES, int TW>
 __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapArgs a) {
   constexpr int STEPS = D / 32;
@@ -124,6 +126,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
   const int tph = a.obs / 16;  // row tiles per q head
   const int rows_all = a.Hq * a.obs;
   const float c = a.scale_log2;
+  const bool hp_pow2 = (a.hp & (a.hp - 1)) == 0;
 
   if constexpr (SCORES)
     for (int i = tid; i < (t1 - t0) * kSnapTile; i += blockDim.x) lds.colmax[i] = 0.f;
@@ -168,113 +171,152 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
         pre[i] = off >= 0 ? ld16(a.k + off + 8 * (cc % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
       }
     };
-    fetch(t0);
-    for (int ti = t0; ti < t1; ++ti) {
-      __syncthreads();  // every wave is done with the previous tile (and its colpart)
+    auto stash = [&](int buf) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int cc = tid + i * 64 * kSnapWaves;
-        *reinterpret_cast<u32x4*>(&lds.kt[(cc / (D / 8)) * SnapLds<D>::kPitch + 8 * (cc % (D / 8))]) = pre[i];
+        *reinterpret_cast<u32x4*>(&lds.kt[buf][(cc / (D / 8)) * SnapLds<D>::kPitch + 8 * (cc % (D / 8))]) = pre[i];
       }
-      __syncthreads();
-      if (ti + 1 < t1) fetch(ti + 1);  // in flight while this tile is reduced
+    };
 
+    __syncthreads();  // the previous unit is done with both buffers
+    fetch(t0);
+    stash(0);
+    if (t0 + 1 < t1) fetch(t0 + 1);
+    __syncthreads();
+    for (int ti = t0; ti < t1; ++ti) {
+      const int buf = (ti - t0) & 1;
       const int kbase = ti * kSnapTile;
-      // S tiles, one 16-key column tile at a time: its B operands (key l16, dims
-      // 8*lg + 32*st) are read from LDS once and used by every row tile.
-      f32x4 acc[TW][4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        u32x4 kb[STEPS];
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st)
-          kb[st] = *reinterpret_cast<const u32x4*>(&lds.kt[(ct * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
-#pragma unroll
-        for (int k = 0; k < TW; ++k) {
-          acc[k][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int st = 0; st < STEPS; ++st) acc[k][ct] = mfma16x16x32<DT>(qa[k][st], kb[st], acc[k][ct]);
-        }
-      }
       // Keys at or past the padded end (only in the last tile of an item) are masked;
       // a 16-key column tile is either wholly valid or wholly masked (aligned % 16 == 0).
       const bool full = kbase + kSnapTile <= a.aligned;
-      bool cvalid[4];
+      // Row tiles in groups of KC (register budget): S for the group, one 16-key column
+      // tile at a time (B operands: key l16, dims 8*lg + 32*st, read from LDS), then its
+      // reduction.
+      constexpr int KC = TW < 2 ? TW : 2;
+      float colacc[4] = {0.f, 0.f, 0.f, 0.f};  // pass 2: this wave's current run
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) cvalid[ct] = full || kbase + 16 * ct < a.aligned;
-
-      if constexpr (!SCORES) {
-        // This lane's max over its valid keys of the tile, per row (column tile 0 is always valid).
-        auto tile_max = [&](int k, int r) {
-          float x = acc[k][0][r];
+      for (int k0 = 0; k0 < TW; k0 += KC) {
+        f32x4 acc[KC][4];
 #pragma unroll
-          for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[k][ct][r]) : x;
-          return x * c;
+        for (int ct = 0; ct < 4; ++ct) {
+          u32x4 kb[STEPS];
+#pragma unroll
+          for (int st = 0; st < STEPS; ++st)
+            kb[st] = *reinterpret_cast<const u32x4*>(
+                &lds.kt[buf][(ct * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
+#pragma unroll
+          for (int kk = 0; kk < KC; ++kk) {
+            acc[kk][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < STEPS; ++st)
+              acc[kk][ct] = mfma16x16x32<DT>(qa[k0 + kk][st], kb[st], acc[kk][ct]);
+          }
+        }
+        auto reduce_group = [&](auto masked_tag) {
+          constexpr bool MASKED = decltype(masked_tag)::value;
+          bool cvalid[4];
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct) cvalid[ct] = !MASKED || kbase + 16 * ct < a.aligned;
+          if constexpr (!SCORES) {
+            // This lane's max over its valid keys of the tile, per row (column tile 0 is always valid).
+            auto tile_max = [&](int kk, int r) {
+              float x = acc[kk][0][r];
+#pragma unroll
+              for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[kk][ct][r]) : x;
+              return x * c;
+            };
+            bool grp_up = false;
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) grp_up |= tile_max(kk, r) > m[k0 + kk][r] + kTau;
+            if (__any(grp_up)) {
+#pragma unroll
+              for (int kk = 0; kk < KC; ++kk)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float mn = fmaxf(m[k0 + kk][r], tile_max(kk, r));
+                  lsum[k0 + kk][r] *= fast_exp2(m[k0 + kk][r] - mn);
+                  m[k0 + kk][r] = mn;
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float e = 0.f;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                  const float p = fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -m[k0 + kk][r]));
+                  e += cvalid[ct] ? p : 0.f;
+                }
+                lsum[k0 + kk][r] += e;
+              }
+          } else {
+            // Column sums over the rows of each run of this wave's tiles that share a head.
+#pragma unroll
+            for (int kk = 0; kk < KC; ++kk) {
+              const int k = k0 + kk;
+              const int tile = wv * TW + k;
+              if (tile >= T) break;  // wave-uniform
+#pragma unroll
+              for (int ct = 0; ct < 4; ++ct) {
+                float x = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x += fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -m[k][r]));
+                colacc[ct] += cvalid[ct] ? x : 0.f;
+              }
+              const bool last_of_run = k == TW - 1 || tile + 1 >= T || (tile + 1) % tph == 0;
+              if (last_of_run) {
+                float v[4];
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                  float x = colacc[ct];
+                  x += __shfl_xor(x, 16);
+                  x += __shfl_xor(x, 32);
+                  v[ct] = x;
+                  colacc[ct] = 0.f;
+                }
+                // The run's first tile holds the run's sums (key `lane` of this tile).
+                const int first = max(wv * TW, (tile / tph) * tph);
+                lds.colpart[buf][first][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
+              }
+            }
+          }
         };
-        bool up = false;
-#pragma unroll
-        for (int k = 0; k < TW; ++k)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) up |= tile_max(k, r) > m[k][r] + kTau;
-        if (__any(up)) {
-#pragma unroll
-          for (int k = 0; k < TW; ++k)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float mn = fmaxf(m[k][r], tile_max(k, r));
-              lsum[k][r] *= fast_exp2(m[k][r] - mn);
-              m[k][r] = mn;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < TW; ++k)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float e = 0.f;
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-              const float p = fast_exp2(__builtin_fmaf(acc[k][ct][r], c, -m[k][r]));
-              e += cvalid[ct] ? p : 0.f;
-            }
-            lsum[k][r] += e;
-          }
-      } else {
-        // Column sums over the rows of each run of this wave's tiles that share a head.
-        float colacc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < TW; ++k) {
-          const int tile = wv * TW + k;
-          if (tile >= T) break;  // wave-uniform
-#pragma unroll
-          for (int ct = 0; ct < 4; ++ct) {
+        if (full)
+          reduce_group(std::false_type{});
+        else
+          reduce_group(std::true_type{});
+        __builtin_amdgcn_sched_barrier(0);  // keep one group's accumulators live at a time
+      }
+
+      // Next tile into the other buffer (last read two tiles ago, before the previous barrier).
+      if (ti + 1 < t1) stash(buf ^ 1);
+      __syncthreads();  // tile ti+1 and this tile's column sums are visible
+      if (ti + 2 < t1) fetch(ti + 2);
+
+      if constexpr (SCORES) {
+        // Per (key, head): add the head's runs (fixed order); max over the unit's heads.
+        if (hp_pow2) {
+          if (tid < kSnapTile * a.hp) {
+            const int key = tid / a.hp, h = tid % a.hp;
             float x = 0.f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x += fast_exp2(__builtin_fmaf(acc[k][ct][r], c, -m[k][r]));
-            colacc[ct] += cvalid[ct] ? x : 0.f;
-          }
-          const bool last_of_run = k == TW - 1 || tile + 1 >= T || (tile + 1) % tph == 0;
-          if (last_of_run) {
-            float v[4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-              float x = colacc[ct];
-              x += __shfl_xor(x, 16);
-              x += __shfl_xor(x, 32);
-              v[ct] = x;
-              colacc[ct] = 0.f;
+            for (int q = h * tph; q < (h + 1) * tph; ++q)
+              if (q == h * tph || q % TW == 0) x += lds.colpart[buf][q][key];
+            for (int o = 1; o < a.hp; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // hp consecutive lanes
+            if (h == 0) {
+              const int j = kbase + key - key0;
+              lds.colmax[j] = fmaxf(lds.colmax[j], x);
             }
-            // The run's first tile holds the run's sums (key `lane` of this tile).
-            const int first = max(wv * TW, (tile / tph) * tph);
-            lds.colpart[first][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
           }
-        }
-        __syncthreads();
-        if (tid < kSnapTile) {
+        } else if (tid < kSnapTile) {
           float mx = 0.f;
           for (int h = 0; h < a.hp; ++h) {
             float x = 0.f;
             for (int q = h * tph; q < (h + 1) * tph; ++q)
-              if (q == h * tph || q % TW == 0) x += lds.colpart[q][tid];  // run starts, fixed order
+              if (q == h * tph || q % TW == 0) x += lds.colpart[buf][q][tid];
             mx = fmaxf(mx, x);
           }
           const int j = kbase + tid - key0;
