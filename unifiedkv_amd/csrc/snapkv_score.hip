@@ -40,6 +40,13 @@
 
 namespace ukv {
 
+#ifndef UKV_SNAP_KC
+#define UKV_SNAP_KC 2  // row tiles per register group
+#endif
+#ifndef UKV_SNAP_SCHED_BARRIER
+#define UKV_SNAP_SCHED_BARRIER 1  // keep the groups apart in the schedule
+#endif
+
 constexpr int kSnapWaves = 8;
 constexpr int kSnapTile = 64;      // keys per LDS tile
 constexpr int kSnapMaxTW = 4;      // row tiles of 16 per wave -> at most 512 rows per unit
@@ -85,6 +92,15 @@ __device__ __forceinline__ int64_t key_row(const SnapArgs& a, int item, int j, i
   return off;
 }
 
+// x summed over the lanes l, l^16, l^32, l^48 (the 4 lane groups of a wave),
+// with the gfx950 cross-row swaps (no LDS traffic).
+__device__ __forceinline__ float sum_lane_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // x + x^16
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);  // + the other 32-lane half
+}
+
 template <int D> struct SnapLds {
   static constexpr int kPitch = D + 16;  // elements per key row in LDS
   alignas(16) uint16_t kt[2][kSnapTile * kPitch];  // double-buffered K tiles (ds_read_b128 / ds_write_b128)
@@ -97,9 +113,10 @@ template <int D> struct SnapLds {
 // Lane l of a wave holds, for each of its row tiles k, query rows 4*(l/16) + r
 // (r < 4) of key column l%16 in each 16-key column tile ct.
 //   pass 1 keeps a running (max, sum) per lane and row over the lane's own keys:
-//          the max moves only when a wave-wide vote finds a score above it by
-//          more than 2^8 (weights stay <= 256), and the 16 lanes of a row are
-//          merged once per range, not per tile;
+//          the tile's weights are computed under the current max, and only when a
+//          wave-wide vote finds a row whose weights exceed 2^8 (or overflow, as on
+//          the first tile) is the exact tile max taken and the row rescaled; the 16
+//          lanes of a row are merged once per range, not per tile;
 //   pass 2 gets m' = m + log2(l) per row, so p = exp2(s * scale - m') is one
 //          FMA and one exp2; each lane adds its p over the rows of its tiles that
 //          belong to one head, then the 4 lane groups are summed; the runs of a
@@ -110,7 +127,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
   constexpr int STEPS = D / 32;
   constexpr int CHUNKS = kSnapTile * D / 8;  // 16-byte chunks per K tile
   constexpr int CPT = CHUNKS / (64 * kSnapWaves);
-  constexpr float kTau = 8.f;
+  constexpr float kTauWeight = 256.f;  // pass 1 keeps every weight at or below 2^8
   static_assert(CHUNKS % (64 * kSnapWaves) == 0, "tile chunks must divide over the threads");
   __shared__ SnapLds<D> lds;
 
@@ -193,7 +210,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
       // Row tiles in groups of KC (register budget): S for the group, one 16-key column
       // tile at a time (B operands: key l16, dims 8*lg + 32*st, read from LDS), then its
       // reduction.
-      constexpr int KC = TW < 2 ? TW : 2;
+      constexpr int KC = TW < UKV_SNAP_KC ? TW : UKV_SNAP_KC;
       float colacc[4] = {0.f, 0.f, 0.f, 0.f};  // pass 2: this wave's current run
 #pragma unroll
       for (int k0 = 0; k0 < TW; k0 += KC) {
@@ -219,40 +236,43 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
 #pragma unroll
           for (int ct = 0; ct < 4; ++ct) cvalid[ct] = !MASKED || kbase + 16 * ct < a.aligned;
           if constexpr (!SCORES) {
-            // This lane's max over its valid keys of the tile, per row (column tile 0 is always valid).
-            auto tile_max = [&](int kk, int r) {
-              float x = acc[kk][0][r];
+            // This lane's weights of the tile's keys under its current max, per row.
+            auto weights = [&](int kk, int r, float mref) {
+              float e = 0.f;
 #pragma unroll
-              for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[kk][ct][r]) : x;
-              return x * c;
+              for (int ct = 0; ct < 4; ++ct) {
+                const float p = fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -mref));
+                e += cvalid[ct] ? p : 0.f;
+              }
+              return e;
             };
-            bool grp_up = false;
+            float e[KC][4];
+            bool over = false;  // some row's weights exceed 2^tau (or are inf: first tile, m = -inf)
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk)
 #pragma unroll
-              for (int r = 0; r < 4; ++r) grp_up |= tile_max(kk, r) > m[k0 + kk][r] + kTau;
-            if (__any(grp_up)) {
+              for (int r = 0; r < 4; ++r) {
+                e[kk][r] = weights(kk, r, m[k0 + kk][r]);
+                over |= !(e[kk][r] <= kTauWeight);
+              }
+            if (__any(over)) {  // rare: move every row's max to its exact running max
 #pragma unroll
               for (int kk = 0; kk < KC; ++kk)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float mn = fmaxf(m[k0 + kk][r], tile_max(kk, r));
+                  float x = acc[kk][0][r];  // column tile 0 is always valid
+#pragma unroll
+                  for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[kk][ct][r]) : x;
+                  const float mn = fmaxf(m[k0 + kk][r], x * c);
                   lsum[k0 + kk][r] *= fast_exp2(m[k0 + kk][r] - mn);
                   m[k0 + kk][r] = mn;
+                  e[kk][r] = weights(kk, r, mn);
                 }
             }
 #pragma unroll
             for (int kk = 0; kk < KC; ++kk)
 #pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                float e = 0.f;
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                  const float p = fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -m[k0 + kk][r]));
-                  e += cvalid[ct] ? p : 0.f;
-                }
-                lsum[k0 + kk][r] += e;
-              }
+              for (int r = 0; r < 4; ++r) lsum[k0 + kk][r] += e[kk][r];
           } else {
             // Column sums over the rows of each run of this wave's tiles that share a head.
 #pragma unroll
@@ -272,10 +292,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
                 float v[4];
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct) {
-                  float x = colacc[ct];
-                  x += __shfl_xor(x, 16);
-                  x += __shfl_xor(x, 32);
-                  v[ct] = x;
+                  v[ct] = sum_lane_groups(colacc[ct]);
                   colacc[ct] = 0.f;
                 }
                 // The run's first tile holds the run's sums (key `lane` of this tile).
@@ -289,7 +306,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
           reduce_group(std::false_type{});
         else
           reduce_group(std::true_type{});
-        __builtin_amdgcn_sched_barrier(0);  // keep one group's accumulators live at a time
+        if constexpr (UKV_SNAP_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);  // one group's accumulators live at a time
       }
 
       // Next tile into the other buffer (last read two tiles ago, before the previous barrier).
