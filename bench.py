@@ -27,6 +27,8 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
   --workload step              a 32-layer decode step on the config-2 batch: prologue + fused
                                append/decode per layer, beside the unfused kernels and the
                                reference's call pattern (step_ragged: the config-3 batch)
+  --workload offload_seq       config 5b's volume through the per-sequence offload / prefetch entry
+                               points over the pinned page arena, beside the reference's per-page pattern
   --workload scores            config 5's importance scores computed: SnapKV observation-window
                                block scores for 32 layers x 8 seqs at 32K (TFLOP/s vs MFMA peak)
   --workload prefill           config 4: chunked prefill, 4 x (16384 prefix + 2048 chunk),
@@ -523,6 +525,104 @@ def run_offload(args, dev):
     }
 
 
+def run_offload_seq(args, dev):
+    """Config 5b's volume through the per-sequence entry points (offload_sequence_blocks /
+    prefetch_sequence_blocks over the pinned page arena): 8 sequences x 32 layers, the 1629
+    non-retained logical blocks of each sequence out and back. Beside it, a bounded sample of the
+    reference's per-(layer, page) pattern (pinned allocation + small copy per K and per V block,
+    core/offload.py:577-597, 662-680) on the same pool."""
+    import numpy as np
+    import torch
+
+    from unifiedkv_amd.offload import SequenceOffloader
+
+    per = C5["ctx"] // 16
+    n_keep = 419
+    pool, lists, _, _, _ = config5_pool(dev, args.seed, C5["B"] * (per - n_keep))
+    L, B = C5["L"], C5["B"]
+    rng = np.random.default_rng(args.seed)
+    mid = np.arange(C5["sink"] // 16, per - C5["obs"] // 16)
+    evict = {b: sorted(rng.choice(mid, size=per - n_keep, replace=False).tolist()) for b in range(B)}
+    n_blocks = sum(len(v) for v in evict.values())
+    page_bytes = pool.B * pool.num_kv_heads * pool.head_dim * 2
+    nbytes = 2 * L * n_blocks * page_bytes
+    log(f"[bench] offload_seq: {B} sequences, {n_blocks} blocks x {L} layers, {nbytes / 1e9:.2f} GB each way")
+    t0 = time.perf_counter()
+    off = SequenceOffloader(pool, arena_pages=n_blocks, chunk_pages=256)
+    arena_s = time.perf_counter() - t0
+    for b in range(B):
+        off.add_sequence(b, lists[b], C5["ctx"])
+    pool.cpu_budget = 2 * nbytes
+
+    def round_trip():
+        a = torch.cuda.Event(enable_timing=True)
+        m = torch.cuda.Event(enable_timing=True)
+        z = torch.cuda.Event(enable_timing=True)
+        a.record(off.stream)
+        for b in range(B):
+            assert off.offload_sequence_blocks(b, evict[b])
+        m.record(off.stream)
+        for b in range(B):
+            assert off.finalize_offload(b, force_sync=True)
+        for b in range(B):
+            assert off.prefetch_sequence_blocks(b, evict[b]) is False
+        z.record(off.stream)
+        for b in range(B):
+            assert off.finalize_prefetch(b, force_sync=True)
+        return a.elapsed_time(m), m.elapsed_time(z)
+
+    before = [pool.k_cache[5, lists[1][evict[1][7]]].clone(), pool.v_cache[30, lists[6][evict[6][100]]].clone()]
+    round_trip()  # warm-up
+    runs = [round_trip() for _ in range(max(1, min(args.steps, 3)))]
+    off_ms = sorted(r[0] for r in runs)[len(runs) // 2]
+    pre_ms = sorted(r[1] for r in runs)[len(runs) // 2]
+    after = [pool.k_cache[5, off.gpu_block_map(1, 5)[evict[1][7]]], pool.v_cache[30, off.gpu_block_map(6, 30)[evict[6][100]]]]
+    ok = all(torch.equal(x.view(torch.int16), y.view(torch.int16)) for x, y in zip(before, after))
+
+    # The reference's per-page pattern on a bounded sample: 48 blocks of sequence 0, all layers.
+    sample = evict[0][:48]
+    ids = [off.gpu_block_map(0, l) for l in range(L)]
+    side = torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    host = []
+    with torch.cuda.stream(side):
+        for l in range(L):
+            for i in sample:
+                bid = ids[l][i]
+                K_g = pool.k_cache[l, bid].transpose(0, 1)
+                V_g = pool.v_cache[l, bid].transpose(0, 1)
+                K_c = torch.empty_like(K_g, device="cpu", pin_memory=True)
+                V_c = torch.empty_like(V_g, device="cpu", pin_memory=True)
+                K_c.copy_(K_g, non_blocking=True)
+                V_c.copy_(V_g, non_blocking=True)
+                host.append((K_c, V_c))
+    side.synchronize()
+    ref_s = time.perf_counter() - t0
+    ref_bytes = 2 * L * len(sample) * page_bytes
+    gbps_off = nbytes / (off_ms * 1e-3) / 1e9
+    gbps_pre = nbytes / (pre_ms * 1e-3) / 1e9
+    return {
+        "metric": "Config 5b volume through offload_sequence_blocks / prefetch_sequence_blocks (pinned arena), GB/s each way",
+        "value": round(2 * nbytes / ((off_ms + pre_ms) * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": len(runs), "warmup": 1, "ms_per_step": round(off_ms + pre_ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "offload_seq_config5b", "layers": L, "batch": B, "blocks_per_sequence": per - n_keep,
+                   "bytes_each_way": nbytes, "arena_pages": n_blocks},
+        "bit_exact": bool(ok),
+        "offload_gbps": round(gbps_off, 2), "prefetch_gbps": round(gbps_pre, 2),
+        "arena_alloc_s": round(arena_s, 2),
+        "reference_pattern_sample": {"gbps": round(ref_bytes / ref_s / 1e9, 3), "bytes": ref_bytes,
+                                     "seconds": round(ref_s, 3),
+                                     "sample": "48 blocks x 32 layers of one sequence, offload direction: a pinned "
+                                               "allocation and a copy per K and per V block"},
+        "roofline": {"bound": "host link", "achieved": round(gbps_off, 2), "peak": None, "unit": "GB/s",
+                     "frac": None, "traffic": None,
+                     "note": "see the offload workload for the measured pinned-copy peak (57 GB/s)"},
+        "cpu_baseline": None,
+    }
+
+
 def run_compacted_decode(args, dev):
     import numpy as np
     import torch
@@ -736,7 +836,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill",
-                             "step", "step_ragged", "scores"])
+                             "step", "step_ragged", "scores", "offload_seq"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -783,6 +883,8 @@ def main():
         rec = run_step(args, dev)
     elif args.workload == "scores":
         rec = run_scores(args, dev)
+    elif args.workload == "offload_seq":
+        rec = run_offload_seq(args, dev)
     else:
         rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)

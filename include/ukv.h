@@ -16,6 +16,7 @@
  *                          core/offload.py:1236-1262 prune_sequence_window (pool->pool compaction),
  *                          core/offload.py:163-179, 577-597, 662-680 per-page offload/prefetch copies
  *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
+ *   ukv_copy_2d            core/offload.py:577-597, 662-680 per-page pinned copies (one strided copy per chunk)
  *   ukv_page16_decode_append  core/scheduler.py:401-418 that scatter fused with the decode call
  *   ukv_decode_prologue    core/offload.py:780-866 reserve_decode_slot (table side),
  *                          core/scheduler.py:1092-1160 per-layer table / cache_seqlens build,
@@ -57,6 +58,16 @@ enum ukv_status {
 
 /* Library version, (major << 16) | (minor << 8) | patch. */
 int ukv_version(void);
+
+/*
+ * Asynchronous strided copy of `height` rows of `width` bytes between device memory and pinned
+ * host memory (either direction, hipMemcpy2DAsync with the direction inferred), on `stream`.
+ * The pinned page arena moves a chunk of pages of every layer with one call (one row per layer).
+ * Replaces the per-(layer, page) pinned allocations and small copies of core/offload.py:577-597
+ * (offload) and 662-680 (prefetch).
+ */
+int ukv_copy_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width, size_t height,
+                ukv_stream_t stream);
 
 /* Static text for a ukv_status value. */
 const char* ukv_status_string(int status);

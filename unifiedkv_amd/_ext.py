@@ -37,6 +37,8 @@ SIGNATURES = {
     "ukv_version": (_c_int, []),
     "ukv_status_string": (ctypes.c_char_p, [_c_int]),
     "ukv_page16_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "ukv_copy_2d": (
+        _c_int, [_c_void_p, ctypes.c_size_t, _c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _c_void_p]),
     "ukv_page16_decode": (
         _c_int,
         [

@@ -1,4 +1,7 @@
-// Library-wide entry points of libukv.so: version and status text.
+// Library-wide entry points of libukv.so: version, status text, and the strided
+// host <-> device copy used by the pinned page arena.
+#include <hip/hip_runtime.h>
+
 #include "../../include/ukv.h"
 
 extern "C" int ukv_version(void) { return (0 << 16) | (1 << 8) | 0; }
@@ -16,4 +19,13 @@ extern "C" const char* ukv_status_string(int status) {
     case UKV_ERR_NO_DEVICE: return "no_device";
     default: return "unknown";
   }
+}
+
+extern "C" int ukv_copy_2d(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width,
+                           size_t height, ukv_stream_t stream) {
+  if (width == 0 || height == 0) return UKV_OK;
+  if (!dst || !src || dst_pitch < width || src_pitch < width) return UKV_ERR_INVALID_ARGUMENT;
+  const hipError_t e = hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, height, hipMemcpyDefault,
+                                        reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
 }
