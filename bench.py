@@ -29,6 +29,8 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
                                reference's call pattern (step_ragged: the config-3 batch)
   --workload offload_seq       config 5b's volume through the per-sequence offload / prefetch entry
                                points over the pinned page arena, beside the reference's per-page pattern
+  --workload prefill_pages     config 4's sequences prefilled in 2048-token chunks over 32 layers with
+                               the K/V written straight into pages, beside the reference's KV path
   --workload scores            config 5's importance scores computed: SnapKV observation-window
                                block scores for 32 layers x 8 seqs at 32K (TFLOP/s vs MFMA peak)
   --workload prefill           config 4: chunked prefill, 4 x (16384 prefix + 2048 chunk),
@@ -623,6 +625,104 @@ def run_offload_seq(args, dev):
     }
 
 
+def run_prefill_pages(args, dev):
+    """The prefill KV path of config 4's sequences (4 x 18432 tokens, 9 chunks of 2048, 32 layers):
+    each chunk's K/V written straight into pages (PrefillPages.write; attention excluded), beside
+    the reference's path on the same GPU: a DynamicCache concatenation per chunk and layer
+    (core/engine.py:1826-1854) and, after the last chunk, write_kv_to_blocks' per-page copies
+    (core/pool.py:127-141; timed on a bounded sample and scaled). The reference also stages the
+    finished KV on the host in between (core/engine.py:1856-1882), not timed here."""
+    import torch
+
+    from unifiedkv_amd.pool import PagedKVPool
+    from unifiedkv_amd.prefill import PrefillPages
+
+    B, T, C, L, Hkv, D = C4["B"], C4["prefix"] + C4["chunk"], C4["chunk"], 32, C4["Hkv"], C4["D"]
+    n_chunks = T // C
+    pages = T // 16
+    pool = PagedKVPool(16, L, Hkv, D, torch.bfloat16, num_blocks=B * pages + 64, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    kc = [torch.randn((B * C, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    vc = [torch.randn((B * C, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    nbytes = 2 * B * T * L * Hkv * D * 2  # K and V of every token and layer, written once
+
+    def ours():
+        pool.free_blocks_by_ids([b for b in range(pool.N_total) if b in pool.used_blocks])
+        pp = PrefillPages(pool, B)
+        for ci in range(n_chunks):
+            pp.begin_chunk([C] * B)
+            for layer in range(L):
+                pp.write(layer, kc[(ci + layer) % 4], vc[(ci + layer) % 4])
+            pp.end_chunk()
+        return pp
+
+    ours()
+    torch.cuda.synchronize()
+    runs = []
+    for _ in range(max(1, min(args.steps, 5))):
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        pp = ours()
+        z.record()
+        torch.cuda.synchronize()
+        runs.append(a.elapsed_time(z))
+    ours_ms = sorted(runs)[len(runs) // 2]
+    ok = torch.equal(pool.k_cache[3, pp.page_lists[2][130]].view(torch.int16),
+                     kc[(130 * 16 // C + 3) % 4][2 * C + (130 * 16) % C: 2 * C + (130 * 16) % C + 16].view(torch.int16))
+
+    # Reference: the DynamicCache concatenation of every chunk, per sequence and layer.
+    def concat_all():
+        past_k = [[None] * B for _ in range(L)]
+        past_v = [[None] * B for _ in range(L)]
+        for ci in range(n_chunks):
+            for layer in range(L):
+                k, v = kc[(ci + layer) % 4], vc[(ci + layer) % 4]
+                for b in range(B):
+                    kb = k[b * C:(b + 1) * C].transpose(0, 1).unsqueeze(0)  # [1, H, C, D]
+                    vb = v[b * C:(b + 1) * C].transpose(0, 1).unsqueeze(0)
+                    pk, pv = past_k[layer][b], past_v[layer][b]
+                    past_k[layer][b] = kb.contiguous() if pk is None else torch.cat([pk, kb], dim=-2)
+                    past_v[layer][b] = vb.contiguous() if pv is None else torch.cat([pv, vb], dim=-2)
+        return past_k, past_v
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    past_k, past_v = concat_all()
+    torch.cuda.synchronize()
+    concat_s = time.perf_counter() - t0
+    # write_kv_to_blocks' per-page loop for one layer of one sequence, scaled to all
+    K, V = past_k[0][0][0], past_v[0][0][0]  # [H, T, D]
+    ids = pp.page_lists[0]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i, bid in enumerate(ids):
+        s0, e0 = i * 16, min(T, i * 16 + 16)
+        pool.k_cache[0, bid, :e0 - s0] = K[:, s0:e0].transpose(0, 1)
+        pool.v_cache[0, bid, :e0 - s0] = V[:, s0:e0].transpose(0, 1)
+    torch.cuda.synchronize()
+    wb_s = (time.perf_counter() - t0) * B * L
+    ref_s = concat_s + wb_s
+    gbps = nbytes / (ours_ms * 1e-3) / 1e9
+    return {
+        "metric": "Prefill KV path straight into pages, config 4 sequences (4 x 18432 tokens, 9 chunks, 32 layers), GB/s of K/V",
+        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": len(runs), "warmup": 1,
+        "ms_per_step": round(ours_ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) chunk K/V)",
+        "config": {"workload": "prefill_pages_config4", "batch": B, "tokens": T, "chunk": C, "layers": L,
+                   "num_kv_heads": Hkv, "head_dim": D, "bytes_written": nbytes},
+        "bit_exact_probe": bool(ok),
+        "reference_path_ms": {"dynamic_cache_concat": round(concat_s * 1e3, 1),
+                              "write_kv_to_blocks_per_page_scaled": round(wb_s * 1e3, 1),
+                              "total": round(ref_s * 1e3, 1)},
+        "speedup_vs_reference_path": round(ref_s * 1e3 / ours_ms, 1),
+        "roofline": {"bound": "hbm", "achieved": round(2 * gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(2 * gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "note": "achieved counts the chunk rows read and the page rows written"},
+        "cpu_baseline": None,
+    }
+
+
 def run_compacted_decode(args, dev):
     import numpy as np
     import torch
@@ -836,7 +936,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill",
-                             "step", "step_ragged", "scores", "offload_seq"])
+                             "step", "step_ragged", "scores", "offload_seq", "prefill_pages"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -885,6 +985,8 @@ def main():
         rec = run_scores(args, dev)
     elif args.workload == "offload_seq":
         rec = run_offload_seq(args, dev)
+    elif args.workload == "prefill_pages":
+        rec = run_prefill_pages(args, dev)
     else:
         rec = run_compacted_decode(args, dev)
     print(json.dumps(rec), flush=True)

@@ -9,6 +9,9 @@ Only tests/ may import this module. Each function follows the cited lines of BP-
 * ``kv_append``            core/scheduler.py:401-408 (token at len -> page bt[b, len//16], slot len%16)
 * ``reserve_decode_slots`` core/offload.py:838-866 per sequence in batch order (core/scheduler.py:1101-1104):
                            len % 16 == 0 -> one FIFO page appended to the sequence's block list
+* ``prefill_chunk_pages``  pages for a prefill chunk written straight into the pool: each sequence
+                           takes the FIFO pages its new length needs, in batch order (the pool-side
+                           replacement of register / writeback, core/offload.py:451-470, core/pool.py:127-141)
 * ``decode_steps``         the page16_native decode loop: reserve, per layer table + append + attention
                            over old_len + 1 (core/scheduler.py:1092-1160, 401-418), commit (1247-1265)
 * ``pool_size``            core/pool.py:36-45 (N_total from free memory)
@@ -145,3 +148,17 @@ def decode_steps(allocator, k_pool, v_pool, page_lists, seq_lens, tokens, attend
         outs.append(row)
         lens = lens + 1
     return outs, lens
+
+
+def prefill_chunk_pages(allocator, page_lists, seq_lens, chunk_lens, block_size: int = 16):
+    """Extends page_lists in place; returns the ids each sequence took (empty lists where none)."""
+    need = [max(0, -(-(int(L) + int(c)) // block_size) - len(ids)) for L, c, ids in zip(seq_lens, chunk_lens,
+                                                                                          page_lists)]
+    if sum(need) > allocator.n_free:
+        raise RuntimeError("prefill_pages_alloc_failed")
+    took = []
+    for ids, n in zip(page_lists, need):
+        got = allocator.allocate_blocks(n) if n else []
+        ids.extend(got)
+        took.append(got)
+    return took

@@ -30,6 +30,8 @@ def prefill_dense(q_f, k_f, v_f, block_table, cu_q, kv_lens, *, softmax_scale, n
     B = len(kv_lens)
     for b in range(B):
         C = int(cu_q[b + 1] - cu_q[b])
+        if C == 0:
+            continue  # no queries in this sequence's chunk
         Lk = int(kv_lens[b])
         P = Lk - C
         n_pages = (Lk + 15) // 16

@@ -100,3 +100,113 @@ def chunked_prefill(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k
     write_chunk_kv(k_cache, v_cache, k_new, v_new, block_table, cu_seqlens_q, kv_lens, mc)
     return paged_prefill_attention(q, k_cache, v_cache, block_table, cu_seqlens_q, kv_lens,
                                    softmax_scale=softmax_scale, n_rep=n_rep, max_chunk=mc)
+
+
+class PrefillPages:
+    """Chunked prefill of a batch of sequences straight into the paged pool.
+
+    BP-KV keeps a chunked prefill's past in a DynamicCache (core/engine.py:1826-1854: each
+    chunk's forward concatenates its K/V onto the past of every layer), stages the finished KV
+    on the host and writes it into the pool only after compression (core/engine.py:1856-1882:
+    capture_prefill_kv, post_prefill_compress, then write_kv_to_blocks, core/pool.py:127-141).
+    Here each chunk's K/V land in their 16-token pages as each layer computes them:
+
+    * ``begin_chunk(chunk_lens)`` reserves the pages the chunk needs: for each sequence in batch
+      order, FIFO from the pool, one id per block shared by every layer; if the pool cannot
+      hold the whole chunk nothing is allocated and ``prefill_pages_alloc_failed`` is raised;
+      the block table, ``cu_seqlens_q`` and the new lengths go to the device in one copy each;
+    * ``attention(layer, q, k, v, ...)`` writes the layer's chunk K/V into the pages and runs
+      the paged causal attention (``write`` alone for callers with their own attention);
+    * ``end_chunk()`` commits the lengths.
+
+    ``page_lists`` / ``seq_lens`` are what ``DecodeBatch``, ``snapkv.score_blocks`` and
+    ``compaction.compact`` take next; no dense copy of the prefill KV is ever made.
+    """
+
+    def __init__(self, pool, num_seqs: Optional[int] = None, *, page_lists=None, seq_lens=None):
+        if page_lists is None:
+            page_lists = [[] for _ in range(int(num_seqs or 0))]
+        if seq_lens is None:
+            seq_lens = [0] * len(page_lists)
+        if len(page_lists) != len(seq_lens) or not page_lists:
+            raise ValueError("PrefillPages: one page list and one length per sequence")
+        for ids, L in zip(page_lists, seq_lens):
+            if len(ids) * pool.B < int(L):
+                raise ValueError("PrefillPages: a sequence has fewer pages than its length needs")
+        pool.ensure_allocated()
+        self.pool = pool
+        self.dev = pool.device
+        self._lists = [[int(x) for x in ids] for ids in page_lists]
+        self._lens = [int(x) for x in seq_lens]
+        self._chunk = None
+
+    @property
+    def page_lists(self):
+        return self._lists
+
+    @property
+    def seq_lens(self):
+        return list(self._lens)
+
+    @property
+    def block_table(self) -> torch.Tensor:
+        if self._chunk is None:
+            raise RuntimeError("prefill_chunk_not_open")
+        return self._chunk["bt"]
+
+    def begin_chunk(self, chunk_lens):
+        """Reserve pages for ``chunk_lens[b]`` new tokens of each sequence; returns
+        (block_table, cu_seqlens_q, kv_lens, max_chunk) for the chunk (device tensors, host int)."""
+        if self._chunk is not None:
+            raise RuntimeError("prefill_chunk_already_open")
+        chunk_lens = [int(c) for c in chunk_lens]
+        if len(chunk_lens) != len(self._lists) or any(c < 0 for c in chunk_lens):
+            raise ValueError("PrefillPages: one non-negative chunk length per sequence")
+        B = self.pool.B
+        need = [max(0, -(-(L + c) // B) - len(ids)) for L, c, ids in zip(self._lens, chunk_lens, self._lists)]
+        if sum(need) > self.pool.n_free:
+            raise RuntimeError("prefill_pages_alloc_failed")
+        for ids, n in zip(self._lists, need):
+            if n:
+                ids.extend(self.pool.allocate_blocks(n))
+        width = max(1, max(len(ids) for ids in self._lists))
+        host = torch.zeros((len(self._lists), width), dtype=torch.int32)
+        for i, ids in enumerate(self._lists):
+            if ids:
+                host[i, :len(ids)] = torch.tensor(ids, dtype=torch.int32)
+        cu = [0]
+        for c in chunk_lens:
+            cu.append(cu[-1] + c)
+        kv = [L + c for L, c in zip(self._lens, chunk_lens)]
+        small = torch.tensor(cu + kv, dtype=torch.int32).pin_memory().to(self.dev, non_blocking=True)
+        self._chunk = dict(bt=host.pin_memory().to(self.dev, non_blocking=True), cu=small[:len(cu)],
+                           kv=small[len(cu):], max_chunk=max(chunk_lens), lens=chunk_lens, total=cu[-1])
+        return self._chunk["bt"], self._chunk["cu"], self._chunk["kv"], self._chunk["max_chunk"]
+
+    def _open(self):
+        if self._chunk is None:
+            raise RuntimeError("prefill_chunk_not_open")
+        return self._chunk
+
+    def write(self, layer_id: int, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """The layer's chunk K/V, packed [total_q, H_kv, D] in batch order, into their pages."""
+        c = self._open()
+        if c["total"] == 0:
+            return
+        write_chunk_kv(self.pool.k_cache[layer_id], self.pool.v_cache[layer_id], k_new, v_new, c["bt"], c["cu"],
+                       c["kv"], c["max_chunk"])
+
+    def attention(self, layer_id: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, *,
+                  softmax_scale: float, n_rep: int) -> torch.Tensor:
+        """Write the layer's chunk K/V, then causal attention of q [total_q, H_q, D] over prefix + chunk."""
+        c = self._open()
+        if c["total"] == 0:
+            return torch.empty_like(q)
+        self.write(layer_id, k_new, v_new)
+        return paged_prefill_attention(q, self.pool.k_cache[layer_id], self.pool.v_cache[layer_id], c["bt"], c["cu"],
+                                       c["kv"], softmax_scale=softmax_scale, n_rep=n_rep, max_chunk=c["max_chunk"])
+
+    def end_chunk(self) -> None:
+        c = self._open()
+        self._lens = [L + n for L, n in zip(self._lens, c["lens"])]
+        self._chunk = None
