@@ -555,7 +555,58 @@ struct VarlenWriteArgs {
   const int32_t* cu_q;
   const int32_t* kv_lens;
   int B, H, D, max_blocks, num_pages, vec;
+  int per_shift, h_shift;  // log2(D / 8), log2(H) for the 16-byte path (-1: not powers of two)
 };
+
+// 16-byte path for power-of-two heads and D / 8: block (tb, b) writes 16 chunk tokens of
+// sequence b; 16-byte chunk `it` = (token, head, chunk) by shifts. The two pages the 16
+// positions can touch are read once; each pass issues 8 K and 8 V loads before its stores.
+__global__ void __launch_bounds__(256) kv_write_varlen_vec_kernel(const VarlenWriteArgs a) {
+  constexpr int J = 8;
+  const int b = blockIdx.y;
+  const int q_begin = a.cu_q[b];
+  const int C = a.cu_q[b + 1] - q_begin;
+  const int i0 = blockIdx.x * 16;
+  if (i0 >= C) return;
+  const int cap = a.max_blocks * 16;
+  const int Lk = min(max(a.kv_lens[b], 0), cap);
+  const int P0 = Lk - C;
+  const int blk0 = (P0 + i0) >> 4;  // first page index these 16 positions touch (P0 + i0 >= 0 when valid)
+  const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
+  const int pg0 = (blk0 >= 0 && blk0 < a.max_blocks) ? btrow[blk0] : -1;
+  const int pg1 = (blk0 + 1 >= 0 && blk0 + 1 < a.max_blocks) ? btrow[blk0 + 1] : -1;
+  const int per_mask = (1 << a.per_shift) - 1, h_mask = (1 << a.h_shift) - 1;
+  const int items = 16 << (a.per_shift + a.h_shift);
+  for (int base = 0; base < items; base += J * 256) {
+    u32x4 kx[J], vx[J];
+    uint16_t* kd[J];
+    uint16_t* vd[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int it = base + j * 256 + threadIdx.x;
+      const int c = it & per_mask;
+      const int h = (it >> a.per_shift) & h_mask;
+      const int i = i0 + (it >> (a.per_shift + a.h_shift));
+      const int pos = P0 + i;
+      const int page = ((pos >> 4) == blk0) ? pg0 : pg1;
+      const bool ok = it < items && i < C && pos >= 0 && pos < cap && (unsigned)page < (unsigned)a.num_pages;
+      kd[j] = ok ? a.k_pool + (int64_t)page * a.k_sp + (int64_t)(pos & 15) * a.k_st + (int64_t)h * a.k_sh + 8 * c
+                 : nullptr;
+      vd[j] = ok ? a.v_pool + (int64_t)page * a.v_sp + (int64_t)(pos & 15) * a.v_st + (int64_t)h * a.v_sh + 8 * c
+                 : nullptr;
+      const int64_t src = (int64_t)(q_begin + (ok ? i : i0)) * a.n_st + (int64_t)h * a.n_sh + 8 * c;
+      kx[j] = ok ? *reinterpret_cast<const u32x4*>(a.k_new + src) : u32x4{0u, 0u, 0u, 0u};
+      vx[j] = ok ? *reinterpret_cast<const u32x4*>(a.v_new + src) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (kd[j]) {
+        *reinterpret_cast<u32x4*>(kd[j]) = kx[j];
+        *reinterpret_cast<u32x4*>(vd[j]) = vx[j];
+      }
+    }
+  }
+}
 
 // grid (token blocks of 16, B): block (tb, b) writes 16 chunk tokens of sequence b.
 __global__ void __launch_bounds__(256) kv_write_varlen_kernel(const VarlenWriteArgs a) {
@@ -633,8 +684,18 @@ extern "C" int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const
   a.vec = head_dim % 8 == 0 && al16(k_pool_layer) && al16(v_pool_layer) && al16(k_new) && al16(v_new) &&
           mul8(a.k_sp) && mul8(a.k_st) && mul8(a.k_sh) && mul8(a.v_sp) && mul8(a.v_st) && mul8(a.v_sh) &&
           mul8(a.n_st) && mul8(a.n_sh);
+  auto log2_exact = [](int x) {
+    int s = 0;
+    while ((1 << s) < x) ++s;
+    return (1 << s) == x ? s : -1;
+  };
+  a.per_shift = a.vec ? log2_exact(head_dim / 8) : -1;
+  a.h_shift = log2_exact(num_heads);
   const dim3 grid((max_chunk + 15) / 16, batch);
-  hipLaunchKernelGGL(kv_write_varlen_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  if (a.vec && a.per_shift >= 0 && a.h_shift >= 0)
+    hipLaunchKernelGGL(kv_write_varlen_vec_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(kv_write_varlen_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
 }
 

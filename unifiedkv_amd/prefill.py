@@ -139,6 +139,7 @@ class PrefillPages:
         self._lists = [[int(x) for x in ids] for ids in page_lists]
         self._lens = [int(x) for x in seq_lens]
         self._chunk = None
+        self._strides = None
 
     @property
     def page_lists(self):
@@ -193,8 +194,26 @@ class PrefillPages:
         c = self._open()
         if c["total"] == 0:
             return
-        write_chunk_kv(self.pool.k_cache[layer_id], self.pool.v_cache[layer_id], k_new, v_new, c["bt"], c["cu"],
-                       c["kv"], c["max_chunk"])
+        pool = self.pool
+        if (k_new.dtype != pool.dtype or v_new.dtype != pool.dtype or k_new.device != self.dev
+                or tuple(k_new.shape) != (c["total"], pool.num_kv_heads, pool.head_dim)
+                or k_new.stride() != v_new.stride() or k_new.stride(-1) != 1):
+            # unusual inputs: the general wrapper converts and checks them
+            write_chunk_kv(pool.k_cache[layer_id], pool.v_cache[layer_id], k_new, v_new, c["bt"], c["cu"], c["kv"],
+                           c["max_chunk"])
+            return
+        if self._strides is None:  # the pool's layer strides, fixed for its life
+            kl = pool.k_cache[0]
+            self._strides = (_ext.i64_array(kl.stride()[:3]), _ext.i64_array(pool.v_cache[0].stride()[:3]),
+                             int(pool.k_cache.stride(0)) * pool.k_cache.element_size(),
+                             int(pool.v_cache.stride(0)) * pool.v_cache.element_size())
+        ks, vs, kl_bytes, vl_bytes = self._strides
+        code = _ext.load().ukv_kv_write_varlen(
+            pool.k_cache.data_ptr() + layer_id * kl_bytes, pool.v_cache.data_ptr() + layer_id * vl_bytes, ks, vs,
+            k_new.data_ptr(), v_new.data_ptr(), _ext.i64_array(k_new.stride()[:2]), c["bt"].data_ptr(),
+            int(c["bt"].shape[1]), c["cu"].data_ptr(), c["kv"].data_ptr(), len(self._lists), c["max_chunk"],
+            pool.num_kv_heads, pool.head_dim, pool.N_total, torch.cuda.current_stream(self.dev).cuda_stream)
+        _ext.check(code, "ukv_kv_write_varlen")
 
     def attention(self, layer_id: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, *,
                   softmax_scale: float, n_rep: int) -> torch.Tensor:
