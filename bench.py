@@ -94,8 +94,35 @@ def event_time_ms(fn, steps, warmup=0):
     return region, [a.elapsed_time(b) for a, b in evs]
 
 
+def host_cpu_info():
+    """CPU model, sockets, cores and threads of this host (from /proc/cpuinfo; no child process)."""
+    info = {"model": None, "sockets": None, "cores": None, "threads": os.cpu_count(),
+            "threads_available": len(os.sched_getaffinity(0))}
+    try:
+        phys, cores_per, model = set(), None, None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                phys.add(v)
+            elif k == "cpu cores" and cores_per is None:
+                cores_per = int(v)
+        info["model"] = model
+        info["sockets"] = len(phys) or None
+        if cores_per and phys:
+            info["cores"] = cores_per * len(phys)
+    except OSError:
+        pass
+    return info
+
+
 def cpu_baseline(tc, layout, budget_s: float, seqs=None):
-    """Time the C page-loop oracle on the host on a bounded sample of sequences."""
+    """The reference's decode semantics on this host's CPU, in two forms, all threads and one
+    thread: the C page loop (core/page16_native.py:34-80, OpenMP over (sequence, q head)) and the
+    torch-CPU dense form (_rebuild_pkv's page gather + eager fp32 attention, core/engine.py:
+    4021-4115). Median of 5 runs after 1 warm-up on a bounded sample of whole sequences."""
     import numpy as np
     import torch
 
@@ -103,7 +130,6 @@ def cpu_baseline(tc, layout, budget_s: float, seqs=None):
     from unifiedkv_amd import workloads
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
-    os.environ["OMP_NUM_THREADS"] = str(threads)
     bt = layout["block_table"]
     lens = layout["seqlens"]
     D, Hq, Hkv = layout["D"], layout["Hq"], layout["Hkv"]
@@ -121,34 +147,57 @@ def cpu_baseline(tc, layout, budget_s: float, seqs=None):
         k = tc["k_cache"].index_select(0, idx).view(torch.int16).cpu().numpy().view(np.uint16)
         v = tc["v_cache"].index_select(0, idx).view(torch.int16).cpu().numpy().view(np.uint16)
         q = tc["q"][list(sel)].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-        return q, k, v, workloads.tables_from_pages(rows), np.ascontiguousarray(lens[list(sel)])
+        return q, k, v, workloads.tables_from_pages(rows), np.ascontiguousarray(lens[list(sel)]), len(sel)
 
-    def run(sample):
-        q, k, v, t, l = sample
+    forms = {
+        "c_page_loop": lambda q, k, v, t, l: oracle.page16_decode_pageloop(
+            q, k, v, t, l, softmax_scale=tc["scale"], n_rep=tc["n_rep"], dtype=dt),
+        "torch_dense": lambda q, k, v, t, l: oracle.page16_decode_torch_dense(
+            q, k, v, t, l, softmax_scale=tc["scale"], n_rep=tc["n_rep"], dtype=dt),
+    }
+
+    def set_threads(n):
+        oracle.set_threads(n)
+        torch.set_num_threads(n)
+
+    def timed(fn, sample):
+        q, k, v, t, l, _ = sample
         t0 = time.perf_counter()
-        oracle.page16_decode_pageloop(q, k, v, t, l, softmax_scale=tc["scale"], n_rep=tc["n_rep"], dtype=dt)
+        fn(q, k, v, t, l)
         return time.perf_counter() - t0
 
-    s1 = host_sample(order[:1])
-    t1 = run(s1)
-    nseq = int(max(1, min(len(order), round(2.0 / max(t1, 1e-3)))))
-    sample = s1 if nseq == 1 else host_sample(order[:nseq])
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-        times.append(run(sample))
-    med = sorted(times)[len(times) // 2]
-    sbytes = workloads.decode_bytes(sample[4], nseq, Hq, Hkv, D, sample[3].shape[1])
-    gbps = sbytes / med / 1e9
+    def measure(name, n_thr, target_s):
+        set_threads(n_thr)
+        fn = forms[name]
+        s1 = host_sample(order[:1])
+        t1 = timed(fn, s1)  # also the warm-up
+        nseq = int(max(1, min(len(order), round(target_s / max(t1, 1e-4)))))
+        sample = s1 if nseq == 1 else host_sample(order[:nseq])
+        if nseq > 1:
+            timed(fn, sample)  # warm-up at the sample size
+        times = sorted(timed(fn, sample) for _ in range(5))
+        med = times[2]
+        sbytes = workloads.decode_bytes(sample[4], nseq, Hq, Hkv, D, sample[3].shape[1])
+        return {"gbps": round(sbytes / med / 1e9, 3), "threads": n_thr, "sequences": nseq,
+                "tokens": int(np.sum(sample[4])), "seconds_median": round(med, 4)}
+
+    per = max(0.2, budget_s / 12.0)
+    results = {}
+    for name in forms:
+        results[name] = {"all_threads": measure(name, threads, per), "one_thread": measure(name, 1, per)}
+    set_threads(threads)
+    main = results["c_page_loop"]["all_threads"]
     return {
-        "value": round(gbps, 3),
+        "value": main["gbps"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"C restatement of core/page16_native.py:34-80 (fp32 page loop, OpenMP over "
-                   f"(seq, q head)) on {nseq} of {layout['B']} sequences ({int(np.sum(sample[4]))} tokens), "
-                   f"median of {len(times)} runs"),
-        "seconds_per_sample_run": round(med, 4),
+        "sample": (f"C restatement of core/page16_native.py:34-80 (fp32 page loop, OpenMP over (seq, q head)) "
+                   f"on {main['sequences']} of {layout['B']} sequences ({main['tokens']} tokens), median of 5 "
+                   f"runs after a warm-up; 'forms' adds 1-thread figures and the torch-CPU dense form"),
+        "seconds_per_sample_run": main["seconds_median"],
+        "forms": results,
+        "host": host_cpu_info(),
     }
 
 
@@ -206,6 +255,7 @@ def decode_record(layout, tc, args, workload, metric, *, with_pmc=False, rotate=
             "bound": "hbm", "achieved": round(kern_gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": round(kern_gbps / PEAK_HBM_GBPS, 4), "traffic": pmc_traffic_bytes() if with_pmc else None,
             "kernel_us": round(kern_ms * 1e3, 2),
+            "kernel_us_median": round(sorted(per_ms)[len(per_ms) // 2] * 1e3, 2),
         },
         "cpu_baseline": cpu,
     }

@@ -92,6 +92,8 @@ def _load():
         I = ctypes.c_int
         lib.ukvo_page16_decode.restype = I
         lib.ukvo_page16_decode.argtypes = [P, P, P, P, P, P, I, I, I, I, I, I, I, ctypes.c_float, I, I]
+        lib.ukvo_set_threads.restype = None
+        lib.ukvo_set_threads.argtypes = [I]
         _lib = lib
     return _lib
 
@@ -118,6 +120,38 @@ def page16_decode_pageloop(q, k_cache, v_cache, block_table, seqlens, *, softmax
     if rc != 0:
         raise ValueError("oracle rejected the arguments")
     return out
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of page16_decode_pageloop."""
+    _load().ukvo_set_threads(int(n))
+
+
+def page16_decode_torch_dense(q, k_cache, v_cache, block_table, seqlens, *, softmax_scale, n_rep, dtype):
+    """The dense-fallback formulation on the CPU in torch fp32: for each sequence, gather its pages
+    (``index_select`` as _rebuild_pkv does, core/engine.py:4021-4115), convert to fp32, repeat the
+    KV heads and run eager attention softmax(q K^T * scale) V. Inputs as page16_decode_pageloop;
+    returns fp32 [B, Hq, D]."""
+    import torch
+
+    tdt = torch.bfloat16 if int(dtype) == DT_BF16 else torch.float16
+    kt = torch.from_numpy(np.ascontiguousarray(k_cache, dtype=np.uint16).view(np.int16)).view(tdt)
+    vt = torch.from_numpy(np.ascontiguousarray(v_cache, dtype=np.uint16).view(np.int16)).view(tdt)
+    qt = torch.from_numpy(np.ascontiguousarray(q, dtype=np.uint16).view(np.int16)).view(tdt).float()
+    B, Hq, D = qt.shape
+    Hkv = kt.shape[2]
+    out = torch.empty((B, Hq, D), dtype=torch.float32)
+    for b in range(B):
+        L = int(seqlens[b])
+        n = (L + 15) // 16
+        ids = torch.from_numpy(np.ascontiguousarray(block_table[b, :n], dtype=np.int64))
+        K = kt.index_select(0, ids).reshape(n * 16, Hkv, D)[:L].float().transpose(0, 1)  # [Hkv, L, D]
+        V = vt.index_select(0, ids).reshape(n * 16, Hkv, D)[:L].float().transpose(0, 1)
+        K = K.repeat_interleave(n_rep, dim=0)  # q head h reads KV head h // n_rep
+        V = V.repeat_interleave(n_rep, dim=0)
+        s = torch.bmm(qt[b].unsqueeze(1), K.transpose(1, 2).contiguous()) * softmax_scale  # [Hq, 1, L]
+        out[b] = torch.bmm(torch.softmax(s, dim=-1), V).squeeze(1)
+    return out.numpy()
 
 
 # --------------------------------------------------------------------------

@@ -28,6 +28,7 @@
  */
 #include <float.h>
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -70,6 +71,11 @@ static float f16_to_f32(uint16_t h) {
 static float load_elem(const uint16_t* p, int dtype) { return dtype == 1 ? bf16_to_f32(*p) : f16_to_f32(*p); }
 
 /* Element -> fp32 for a whole buffer (used by the Python side for inputs). */
+/* Threads of the OpenMP page loop (the CPU baseline reports all-core and 1-thread figures). */
+void ukvo_set_threads(int n) {
+  if (n > 0) omp_set_num_threads(n);
+}
+
 void ukvo_to_f32(const uint16_t* src, float* dst, int64_t n, int dtype) {
   for (int64_t i = 0; i < n; ++i) dst[i] = load_elem(src + i, dtype);
 }

@@ -61,6 +61,24 @@ def test_three_formulations_agree(dtype):
     np.testing.assert_allclose(loop, dense, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [oracle.DT_F16, oracle.DT_BF16])
+def test_torch_cpu_dense_form_matches_the_closed_form(dtype):
+    # The CPU baseline's second form (page gather + eager fp32 attention, as _rebuild_pkv).
+    c = small_case(5, dtype=dtype)
+    got = oracle.page16_decode_torch_dense(c["q"], c["k"], c["v"], c["bt"], c["lens"], softmax_scale=c["scale"],
+                                           n_rep=c["n_rep"], dtype=dtype)
+    np.testing.assert_allclose(got, run_dense(c), rtol=1e-5, atol=1e-6)
+
+
+def test_pageloop_is_the_same_with_one_thread():
+    c = small_case(6, dtype=oracle.DT_BF16)
+    oracle.set_threads(1)
+    one = run_loop(c)
+    oracle.set_threads(4)
+    many = run_loop(c)
+    np.testing.assert_array_equal(one, many)  # each (sequence, head) is computed by one thread
+
+
 def test_config1_pageloop_matches_dense():
     case = workloads.numpy_case("tiny", 7)
     c = dict(q=case["q"], k=case["k_cache"], v=case["v_cache"], bt=case["block_table"], lens=case["seqlens"],
