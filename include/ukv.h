@@ -250,8 +250,9 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  *                block_table [seqs, max_blocks] int32: page block_table[b][t / 16], slot t % 16 at
  *                k + l*s0 + page*s1 + slot*s2 + g*s3 (the pool [layers, N, 16, H_kv, D]); page ids
  *                outside [0, num_pages) read as zero rows
- * num_q_heads must equal num_kv_heads * n_rep (q head h reads KV head h / n_rep). The workspace
- * (ukv_snapkv_workspace_bytes) needs no initialisation. Replaces core/scheduler.py:565-592 and the
+ * num_q_heads must equal num_kv_heads * n_rep (q head h reads KV head h / n_rep); block_size must
+ * be 16 (the page size; the reference's SnapKV block); layers * seqs <= 65535; otherwise
+ * UKV_ERR_INVALID_ARGUMENT. The workspace (ukv_snapkv_workspace_bytes) needs no initialisation. Replaces core/scheduler.py:565-592 and the
  * scoring steps of core/compress.py:116-130.
  */
 int ukv_snapkv_block_count(int seq_len, int sink_len, int obs_len, int block_size);

@@ -77,6 +77,40 @@ def test_block_count_entry_point_matches_the_oracle():
         assert snapkv.block_count(L, sink, obs) == want
 
 
+def test_entry_point_rejects_bad_shapes_before_any_launch():
+    import ctypes
+
+    from unifiedkv_amd import _ext
+
+    lib = _ext.load()
+    s3 = _ext.i64_array((0, 8, 8))
+    s4 = _ext.i64_array((0, 0, 8, 8))
+    p = 1 << 20
+
+    def call(**kw):
+        a = dict(layers=1, seqs=1, L=200, sink=16, obs=16, hq=4, hkv=2, d=64, n_rep=2, bs=16, stride=64)
+        a.update(kw)
+        return lib.ukv_snapkv_scores(p, s3, p, s4, None, 0, 0, a["layers"], a["seqs"], a["L"], a["sink"], a["obs"],
+                                     a["hq"], a["hkv"], a["d"], a["n_rep"], a["bs"], ctypes.c_float(0.125),
+                                     _ext.UKV_DTYPE_BF16, p, a["stride"], p, 1 << 30, None)
+
+    assert call(bs=32) == _ext.UKV_ERR_INVALID_ARGUMENT          # blocks are 16-token pages
+    assert call(hq=6) == _ext.UKV_ERR_INVALID_ARGUMENT           # H_q != H_kv * n_rep
+    assert call(layers=300, seqs=300) == _ext.UKV_ERR_INVALID_ARGUMENT
+    assert call(stride=5) == _ext.UKV_ERR_INVALID_ARGUMENT       # row stride below N
+    assert call(L=16 + 16 + 15) == _ext.UKV_OK                   # too short: nothing to do
+    assert lib.ukv_snapkv_workspace_bytes(1, 1, 200, 16, 16, 4, 2, 64, 2, 32) == 0
+
+
+def test_copy_2d_rejects_bad_pitches():
+    from unifiedkv_amd import _ext
+
+    lib = _ext.load()
+    assert lib.ukv_copy_2d(None, 0, None, 0, 0, 5, None) == _ext.UKV_OK       # empty
+    assert lib.ukv_copy_2d(None, 64, 1 << 20, 64, 64, 1, None) == _ext.UKV_ERR_INVALID_ARGUMENT
+    assert lib.ukv_copy_2d(1 << 20, 32, 1 << 21, 64, 64, 2, None) == _ext.UKV_ERR_INVALID_ARGUMENT
+
+
 # ------------------------------------------------------------------------------ GPU
 def _bits(rng, shape, dtype):
     return workloads._round_bits(rng.standard_normal(shape, dtype=np.float32), dtype)

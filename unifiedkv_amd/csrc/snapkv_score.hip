@@ -497,7 +497,7 @@ SnapPlan snap_plan(int items, int seq_len, int sink, int obs, int num_q_heads, i
       p.hp = h;
       break;
     }
-  p.tiled = (head_dim == 64 || head_dim == 128) && obs % 16 == 0 && p.hp > 0 && aligned_rows && block_size == 16;
+  p.tiled = (head_dim == 64 || head_dim == 128) && obs % 16 == 0 && p.hp > 0 && aligned_rows;
   p.parts = p.tiled ? n_rep / p.hp : 1;
   if (p.tiled) {
     const int want = (2 * snap_cu_count() + items - 1) / std::max(1, items);
@@ -559,8 +559,9 @@ bool snap_aligned(const void* q, const void* k, const int64_t* qs, const int64_t
 
 bool snap_shape_ok(int layers, int seqs, int seq_len, int sink, int obs, int num_q_heads, int num_kv_heads,
                    int head_dim, int n_rep, int block_size) {
+  // Blocks are the pool's 16-token pages (the kernels sum scores over 16 keys).
   return layers > 0 && seqs > 0 && seq_len > 0 && sink >= 0 && obs > 0 && num_q_heads > 0 && num_kv_heads > 0 &&
-         head_dim > 0 && n_rep > 0 && block_size > 0 && num_q_heads == num_kv_heads * n_rep;
+         head_dim > 0 && n_rep > 0 && block_size == 16 && num_q_heads == num_kv_heads * n_rep;
 }
 
 }  // namespace
