@@ -47,10 +47,17 @@ namespace ukv {
 #define UKV_SNAP_SCHED_BARRIER 1  // keep the groups apart in the schedule
 #endif
 
-constexpr int kSnapWaves = 8;
-constexpr int kSnapTile = 64;      // keys per LDS tile
-constexpr int kSnapMaxTW = 4;      // row tiles of 16 per wave -> at most 512 rows per unit
-constexpr int kSnapMaxKeys = 8192; // keys per range (LDS running max)
+#ifndef UKV_SNAP_WAVES
+#define UKV_SNAP_WAVES 8  // waves per workgroup
+#endif
+#ifndef UKV_SNAP_MAX_KEYS
+#define UKV_SNAP_MAX_KEYS 8192  // keys per range (LDS running max)
+#endif
+
+constexpr int kSnapWaves = UKV_SNAP_WAVES;
+constexpr int kSnapTile = 64;                     // keys per LDS tile
+constexpr int kSnapMaxTW = 4;                     // row tiles of 16 per wave
+constexpr int kSnapMaxKeys = UKV_SNAP_MAX_KEYS;
 
 struct SnapArgs {
   const uint16_t* q;  // [items][H_q][obs][D] with strides q_si, q_sh, q_st
@@ -123,7 +130,7 @@ template <int D> struct SnapLds {
 //          head are added and the max over heads taken by 64 * hp threads.
 // K tiles and column sums are double-buffered: one barrier per tile.
 template <int DT, int D, bool SCORES, int TW>
-__global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapArgs a) {
+__global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const SnapArgs a) {
   constexpr int STEPS = D / 32;
   constexpr int CHUNKS = kSnapTile * D / 8;  // 16-byte chunks per K tile
   constexpr int CPT = CHUNKS / (64 * kSnapWaves);
@@ -316,7 +323,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves) snap_tile_kernel(const SnapAr
 
       if constexpr (SCORES) {
         // Per (key, head): add the head's runs (fixed order); max over the unit's heads.
-        if (hp_pow2) {
+        if (hp_pow2 && kSnapTile * a.hp <= (int)blockDim.x) {
           if (tid < kSnapTile * a.hp) {
             const int key = tid / a.hp, h = tid % a.hp;
             float x = 0.f;
