@@ -65,20 +65,6 @@ __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
-__device__ __forceinline__ uint32_t pack_f16(float x0, float x1) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, f16x2));
-}
-__device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
-}
-
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ u16x2 as_u16x2(uint32_t w) { return __builtin_bit_cast(u16x2, w); }
-
 // Two bf16 values -> two fp16 values (RNE; exact when 2^-14 <= |x| < 65520),
 // folding the magnitude bits of both into amag (bf16 magnitudes above 0x477F,
 // i.e. |x| >= 65536, inf and NaN, do not fit fp16).

@@ -6,25 +6,26 @@
 //   A     = softmax(Q_obs . repeat_kv(K_mid)^T * scale)      [H_q, obs, aligned]
 //   s     = A.mean(over obs queries).max(over q heads)       [aligned]
 //   block = s.view(N, block).sum(-1);  maxpool1d(k=3, s=1, p=1) when N >= 3
-// in fp32 from 16-bit Q and K (the reference runs these steps in the model
-// dtype; here every intermediate is fp32).
+// from 16-bit Q and K (the reference runs these steps in the model dtype).
+// Scores, maxima and sums are fp32; each softmax weight is rounded to fp16
+// (relative error <= 2^-11, scaled by a power of two away from fp16's subnormal
+// range) where the matrix cores sum it.
 //
 // Work decomposition: an item's mid keys form Kt tiles of 64 keys, split into
 // S contiguous ranges; one workgroup (8 waves) per (range, item). A unit is
 // one KV group's q heads, or part of them when n_rep * obs > 512 rows: the
 // unit's Q rows (up to 512 = 8 waves x 4 tiles of 16) stay in registers while
 // its K tiles stream through LDS (64 keys, 16-byte rows loaded once per
-// workgroup, padded pitch against bank conflicts). S = Q K^T runs on
-// v_mfma_f32_16x16x32 (A = 16 query rows, B = 16 keys: lane l holds query rows
-// 4*(l/16)+r of key l%16).
+// workgroup, padded pitch against bank conflicts). The scores run on
+// v_mfma_f32_16x16x32.
 //   pass 1 (stats): per query row, running max and sum of exp2 over the
 //           range's keys -> partial (m, l) per (range, row); a small kernel
-//           merges the ranges into (m, 1/l);
-//   pass 2 (scores): p = exp2(s - m) / l, summed over each head's queries
-//           (per-lane, then across the 4 lane groups, then the head's row tiles
-//           in a fixed order through LDS, so results are reproducible), max
-//           over heads, running max over units per key in LDS, then the sums
-//           over 16-key blocks of the range;
+//           merges the ranges into m' = m + log2(l);
+//   pass 2 (scores): p = exp2(s - m'), summed over each head's queries (on
+//           the matrix cores per wave, then the head's waves in a fixed order
+//           through LDS, so results are reproducible), max over heads, running
+//           max over units per key in LDS, then the sums over 16-key blocks of
+//           the range;
 //   finish: the 3-wide max pool over each item's blocks.
 // Both passes compute Q K^T, so the cost is 2 * (2 * H_q * obs * aligned * D)
 // FLOPs per item on the matrix cores; K is read twice.
@@ -40,12 +41,6 @@
 
 namespace ukv {
 
-#ifndef UKV_SNAP_KC
-#define UKV_SNAP_KC 2  // row tiles per register group
-#endif
-#ifndef UKV_SNAP_SCHED_BARRIER
-#define UKV_SNAP_SCHED_BARRIER 1  // keep the groups apart in the schedule
-#endif
 
 #ifndef UKV_SNAP_WAVES
 #define UKV_SNAP_WAVES 8  // waves per workgroup
@@ -62,10 +57,10 @@ constexpr int kSnapMaxKeys = UKV_SNAP_MAX_KEYS;
 struct SnapArgs {
   const uint16_t* q;  // [items][H_q][obs][D] with strides q_si, q_sh, q_st
   int64_t q_si, q_sh, q_st;
-  const uint16_t* k;  // token t, head g of item (b, l): see key_row()
+  const uint16_t* k;  // token t, head g of item (b, l): see key_row() (pages hold 16 tokens)
   int64_t k_sl, k_sb, k_st, k_sh;
   const int32_t* table;  // [seqs][max_blocks] or null (dense)
-  int max_blocks, num_pages, page_size;
+  int max_blocks, num_pages;
   int layers, items;
   int sink, obs, L_mid, aligned, n_blocks;
   int Hq, Hkv, n_rep, D;
@@ -88,53 +83,59 @@ __device__ __forceinline__ int64_t key_row(const SnapArgs& a, int item, int j, i
   const int t = a.sink + j;
   int64_t off = (int64_t)l * a.k_sl + (int64_t)g * a.k_sh;
   if (a.table) {
-    const int blk = t / a.page_size;
+    const int blk = t >> 4;
     if (blk >= a.max_blocks) return -1;
     const int page = a.table[(int64_t)b * a.max_blocks + blk];
     if ((unsigned)page >= (unsigned)a.num_pages) return -1;
-    off += (int64_t)page * a.k_sb + (int64_t)(t % a.page_size) * a.k_st;
+    off += (int64_t)page * a.k_sb + (int64_t)(t & 15) * a.k_st;
   } else {
     off += (int64_t)b * a.k_sb + (int64_t)t * a.k_st;
   }
   return off;
 }
 
-// x summed over the lanes l, l^16, l^32, l^48 (the 4 lane groups of a wave),
+// Max of x over the lanes l, l^16, l^32, l^48 (the 4 lane groups of a wave),
 // with the gfx950 cross-row swaps (no LDS traffic).
-__device__ __forceinline__ float sum_lane_groups(float x) {
+__device__ __forceinline__ float max_lane_groups(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // x + x^16
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));  // x, x^16
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);  // + the other 32-lane half
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));  // and the other 32-lane half
 }
 
 template <int D> struct SnapLds {
   static constexpr int kPitch = D + 16;  // elements per key row in LDS
   alignas(16) uint16_t kt[2][kSnapTile * kPitch];  // double-buffered K tiles (ds_read_b128 / ds_write_b128)
-  float colpart[2][32][kSnapTile];       // double-buffered column sums per run of row tiles (<= 32 tiles)
+  float colpart[2][32][kSnapTile];       // double-buffered column sums per wave, at its first row tile
   float colmax[kSnapMaxKeys];            // running max over units, per key of the range
 };
 
-// TW: row tiles of 16 per wave (1, 2 or 4), the smallest that covers the unit.
+// TW: row tiles of 16 per wave (1, 2 or 4); TW divides the tiles of one q head,
+// so a wave's tiles belong to one head.
 //
-// Lane l of a wave holds, for each of its row tiles k, query rows 4*(l/16) + r
-// (r < 4) of key column l%16 in each 16-key column tile ct.
-//   pass 1 keeps a running (max, sum) per lane and row over the lane's own keys:
-//          the tile's weights are computed under the current max, and only when a
-//          wave-wide vote finds a row whose weights exceed 2^8 (or overflow, as on
-//          the first tile) is the exact tile max taken and the row rescaled; the 16
-//          lanes of a row are merged once per range, not per tile;
-//   pass 2 gets m' = m + log2(l) per row, so p = exp2(s * scale - m') is one
-//          FMA and one exp2; each lane adds its p over the rows of its tiles that
-//          belong to one head, then the 4 lane groups are summed; the runs of a
-//          head are added and the max over heads taken by 64 * hp threads.
+//   pass 1 (S^T: lane l holds keys 4*(l/16) + r of column tile ct for query
+//          column l%16 of row tile k) keeps a running max per query column, the
+//          same in the 4 lane groups. A step's weights are computed under the
+//          current max; only when a wave-wide vote finds one above 2^8 (or an
+//          overflow, as on the first tile) is the exact max taken and the column
+//          rescaled. The weights are summed over keys on the matrix cores: as fp16
+//          B operand against an all-ones A, every row of the result is the sum.
+//   pass 2 (S: lane l holds query rows 4*(l/16) + r of key l%16) gets
+//          m' = m + log2(l) per row, so p = exp2(s * scale - m') is one FMA and
+//          one exp2; the weights are summed over the wave's rows on the matrix
+//          cores (fp16 B operand against a one-hot selector A that puts column
+//          tile ct's sums into row 4*ct); the waves of a head are added and the
+//          max over heads taken by 64 * hp threads.
 // K tiles and column sums are double-buffered: one barrier per tile.
 template <int DT, int D, bool SCORES, int TW>
 __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const SnapArgs a) {
   constexpr int STEPS = D / 32;
   constexpr int CHUNKS = kSnapTile * D / 8;  // 16-byte chunks per K tile
   constexpr int CPT = CHUNKS / (64 * kSnapWaves);
-  constexpr float kTauWeight = 256.f;  // pass 1 keeps every weight at or below 2^8
+  // Weights enter the column-sum MFMAs as fp16 times a power of two: pass 1
+  // keeps them at or below 2^8 (2^15 lifted), pass 2's are at most 1 (2^14
+  // lifted); the lift keeps small weights out of fp16's subnormal range.
+  constexpr float kLift1 = 7.f, kLift2 = 14.f, kUnlift2 = 1.f / 16384.f;
   static_assert(CHUNKS % (64 * kSnapWaves) == 0, "tile chunks must divide over the threads");
   __shared__ SnapLds<D> lds;
 
@@ -151,6 +152,15 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
   const int rows_all = a.Hq * a.obs;
   const float c = a.scale_log2;
   const bool hp_pow2 = (a.hp & (a.hp - 1)) == 0;
+  const int hp_log2 = 31 - __builtin_clz(a.hp);
+  const int item_b = item / a.layers, item_l = item - item_b * a.layers;  // sequence, layer
+  const int32_t* trow = a.table ? a.table + (int64_t)item_b * a.max_blocks : nullptr;
+  // MFMA A operands of the column sums (fp16 1.0 pairs): all ones (pass 1), and
+  // rows 0 and 4 selecting dwords 0-1 and 2-3 of the B operand (pass 2).
+  constexpr uint32_t kOnes = 0x3C003C00u;
+  const u32x4 ones = u32x4{kOnes, kOnes, kOnes, kOnes};
+  const u32x4 colsel = u32x4{l16 == 0 ? kOnes : 0u, l16 == 0 ? kOnes : 0u, l16 == 4 ? kOnes : 0u,
+                             l16 == 4 ? kOnes : 0u};
 
   if constexpr (SCORES)
     for (int i = tid; i < (t1 - t0) * kSnapTile; i += blockDim.x) lds.colmax[i] = 0.f;
@@ -161,9 +171,15 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
 
     // This wave's row tiles: w*TW .. w*TW+TW-1 (tiles past T are zero and unused).
     u32x4 qa[TW][STEPS];
-    float m[TW][4], lsum[TW][4];  // pass 1: running max / sum; pass 2: m' = m + log2(l)
+    // pass 1: m[k][0] is the running max (log2 units) of query column l16 of
+    //         tile k, the same in the 4 lane groups, and every row of lsum[k]
+    //         holds 2^kLift1 times the column's running sum of weights;
+    // pass 2: m[k][r] = m' - kLift2 of query row 4*lg + r of tile k.
+    float m[TW][4];
+    f32x4 lsum[TW];
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
+      lsum[k] = f32x4{0.f, 0.f, 0.f, 0.f};
       const int tile = wv * TW + k;
       const bool on = tile < T;
       const int rr = tile * 16 + l16;  // A row of this lane
@@ -173,26 +189,35 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
       for (int st = 0; st < STEPS; ++st) qa[k][st] = on ? ld16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        m[k][r] = -INFINITY;
-        lsum[k][r] = 0.f;
+        m[k][r] = SCORES ? INFINITY : -INFINITY;  // pass 2: rows past the unit weigh 0
         if constexpr (SCORES) {
           if (on) {  // C rows 4*lg + r of the tile
             const int row = tile * 16 + 4 * lg + r;
-            m[k][r] = a.stats[(int64_t)item * rows_all + (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs].x;
+            m[k][r] = a.stats[(int64_t)item * rows_all + (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs].x -
+                      kLift2;
           }
         }
       }
     }
 
     // K tile loads: thread chunk cc = tid + i*512 -> key cc / (D/8), dims 8*(cc % (D/8)).
+    // key_row() with the item's and the unit's terms taken out of the tile loop.
+    const uint16_t* kg = a.k + (int64_t)item_l * a.k_sl + (int64_t)g * a.k_sh;
     u32x4 pre[CPT];
     auto fetch = [&](int tile_idx) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int cc = tid + i * 64 * kSnapWaves;
-        const int key = tile_idx * kSnapTile + cc / (D / 8);
-        const int64_t off = key_row(a, item, key, g);
-        pre[i] = off >= 0 ? ld16(a.k + off + 8 * (cc % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
+        const int j = tile_idx * kSnapTile + cc / (D / 8);  // mid key
+        const int t = a.sink + j;
+        const uint16_t* src = nullptr;
+        if (trow) {
+          const int page = j < a.L_mid && (t >> 4) < a.max_blocks ? trow[t >> 4] : -1;
+          if ((unsigned)page < (unsigned)a.num_pages) src = kg + (int64_t)page * a.k_sb + (int64_t)(t & 15) * a.k_st;
+        } else if (j < a.L_mid) {
+          src = kg + (int64_t)item_b * a.k_sb + (int64_t)t * a.k_st;
+        }
+        pre[i] = src ? ld16(src + 8 * (cc % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto stash = [&](int buf) {
@@ -211,109 +236,125 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
     for (int ti = t0; ti < t1; ++ti) {
       const int buf = (ti - t0) & 1;
       const int kbase = ti * kSnapTile;
-      // Keys at or past the padded end (only in the last tile of an item) are masked;
-      // a 16-key column tile is either wholly valid or wholly masked (aligned % 16 == 0).
-      const bool full = kbase + kSnapTile <= a.aligned;
-      // Row tiles in groups of KC (register budget): S for the group, one 16-key column
-      // tile at a time (B operands: key l16, dims 8*lg + 32*st, read from LDS), then its
-      // reduction.
-      constexpr int KC = TW < UKV_SNAP_KC ? TW : UKV_SNAP_KC;
-      float colacc[4] = {0.f, 0.f, 0.f, 0.f};  // pass 2: this wave's current run
+      // Keys at or past the padded end lie in the last tile of an item only; a
+      // 16-key column tile is either wholly valid or wholly past it (aligned % 16 == 0).
+      // The tile runs in steps j = (half, row tile k): the 32 keys of column tiles
+      // 2*half, 2*half + 1 against row tile k. K operands (key l16 of column tile
+      // ct, dims 8*lg + 32*st) are read from LDS once per half. Pass 2 computes
+      // S = Q K^T (lane: query rows 4*lg + r of key l16), pass 1 S^T = K Q^T (lane:
+      // keys 4*lg + r of query l16); the 16x16x32 A and B operand layouts are the
+      // same, so only the operand order differs. Step j+1's scores are issued on
+      // the matrix cores before step j's weights are computed on the vector ALUs.
+      // pass 2: rows 0 and 4 of colsum[half] hold the column sums of column tiles
+      // 2*half and 2*half + 1 over the wave's row tiles (one q head), i.e.
+      // element 0 of lanes 0-31 of colsum[half].
+      f32x4 colsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      {
+        constexpr int NSTEP = 2 * TW;
+        u32x4 kb[2][STEPS];
+        auto load_half = [&](int hf) {
 #pragma unroll
-      for (int k0 = 0; k0 < TW; k0 += KC) {
-        f32x4 acc[KC][4];
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          u32x4 kb[STEPS];
-#pragma unroll
-          for (int st = 0; st < STEPS; ++st)
-            kb[st] = *reinterpret_cast<const u32x4*>(
-                &lds.kt[buf][(ct * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
-#pragma unroll
-          for (int kk = 0; kk < KC; ++kk) {
-            acc[kk][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
             for (int st = 0; st < STEPS; ++st)
-              acc[kk][ct] = mfma16x16x32<DT>(qa[k0 + kk][st], kb[st], acc[kk][ct]);
-          }
-        }
-        auto reduce_group = [&](auto masked_tag) {
-          constexpr bool MASKED = decltype(masked_tag)::value;
-          bool cvalid[4];
+              kb[c2][st] = *reinterpret_cast<const u32x4*>(
+                  &lds.kt[buf][((2 * hf + c2) * 16 + l16) * SnapLds<D>::kPitch + 8 * lg + 32 * st]);
+        };
+        f32x4 acc[2][2];
+        auto scores = [&](int j, f32x4(&dst)[2]) {
+          const int k = j % TW;
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct) cvalid[ct] = !MASKED || kbase + 16 * ct < a.aligned;
-          if constexpr (!SCORES) {
-            // This lane's weights of the tile's keys under its current max, per row.
-            auto weights = [&](int kk, int r, float mref) {
-              float e = 0.f;
+          for (int c2 = 0; c2 < 2; ++c2) {
+            dst[c2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int ct = 0; ct < 4; ++ct) {
-                const float p = fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -mref));
-                e += cvalid[ct] ? p : 0.f;
-              }
-              return e;
-            };
-            float e[KC][4];
-            bool over = false;  // some row's weights exceed 2^tau (or are inf: first tile, m = -inf)
-#pragma unroll
-            for (int kk = 0; kk < KC; ++kk)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                e[kk][r] = weights(kk, r, m[k0 + kk][r]);
-                over |= !(e[kk][r] <= kTauWeight);
-              }
-            if (__any(over)) {  // rare: move every row's max to its exact running max
-#pragma unroll
-              for (int kk = 0; kk < KC; ++kk)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                  float x = acc[kk][0][r];  // column tile 0 is always valid
-#pragma unroll
-                  for (int ct = 1; ct < 4; ++ct) x = cvalid[ct] ? fmaxf(x, acc[kk][ct][r]) : x;
-                  const float mn = fmaxf(m[k0 + kk][r], x * c);
-                  lsum[k0 + kk][r] *= fast_exp2(m[k0 + kk][r] - mn);
-                  m[k0 + kk][r] = mn;
-                  e[kk][r] = weights(kk, r, mn);
-                }
-            }
-#pragma unroll
-            for (int kk = 0; kk < KC; ++kk)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) lsum[k0 + kk][r] += e[kk][r];
-          } else {
-            // Column sums over the rows of each run of this wave's tiles that share a head.
-#pragma unroll
-            for (int kk = 0; kk < KC; ++kk) {
-              const int k = k0 + kk;
-              const int tile = wv * TW + k;
-              if (tile >= T) break;  // wave-uniform
-#pragma unroll
-              for (int ct = 0; ct < 4; ++ct) {
-                float x = 0.f;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) x += fast_exp2(__builtin_fmaf(acc[kk][ct][r], c, -m[k][r]));
-                colacc[ct] += cvalid[ct] ? x : 0.f;
-              }
-              const bool last_of_run = k == TW - 1 || tile + 1 >= T || (tile + 1) % tph == 0;
-              if (last_of_run) {
-                float v[4];
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                  v[ct] = sum_lane_groups(colacc[ct]);
-                  colacc[ct] = 0.f;
-                }
-                // The run's first tile holds the run's sums (key `lane` of this tile).
-                const int first = max(wv * TW, (tile / tph) * tph);
-                lds.colpart[buf][first][lane] = lg == 0 ? v[0] : lg == 1 ? v[1] : lg == 2 ? v[2] : v[3];
-              }
-            }
+            for (int st = 0; st < STEPS; ++st)
+              dst[c2] = SCORES ? mfma16x16x32<DT>(qa[k][st], kb[c2][st], dst[c2])
+                               : mfma16x16x32<DT>(kb[c2][st], qa[k][st], dst[c2]);
           }
         };
-        if (full)
-          reduce_group(std::false_type{});
-        else
-          reduce_group(std::true_type{});
-        if constexpr (UKV_SNAP_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);  // one group's accumulators live at a time
+        load_half(0);
+        scores(0, acc[0]);
+#pragma unroll
+        for (int j = 0; j < NSTEP; ++j) {
+          const int hf = j / TW, k = j % TW;
+          if (j + 1 < NSTEP) {
+            if ((j + 1) % TW == 0) load_half((j + 1) / TW);
+            scores(j + 1, acc[(j + 1) & 1]);
+          }
+          f32x4(&sc)[2] = acc[j & 1];
+          if constexpr (SCORES) {
+            // Weights times 2^kLift2 as fp16, dword 2*c2 + r/2 = rows r, r+1 of
+            // column tile 2*half + c2 (k = the lane group's rows); the selector
+            // sums dwords 0-1 into row 0 and dwords 2-3 into row 4.
+            // Keys at or past the padded end (zero rows, last tile only) get sums
+            // too, but no block reads them.
+            uint32_t pk[4];
+#pragma unroll
+            for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+              for (int r = 0; r < 4; r += 2) {
+                const float p0 = fast_exp2(__builtin_fmaf(sc[c2][r], c, -m[k][r]));
+                const float p1 = fast_exp2(__builtin_fmaf(sc[c2][r + 1], c, -m[k][r + 1]));
+                pk[2 * c2 + r / 2] = pack_f16(p0, p1);
+              }
+            colsum[hf] = mfma16x16x32<UKV_DTYPE_F16>(colsel, u32x4{pk[0], pk[1], pk[2], pk[3]}, colsum[hf]);
+          } else {
+            // Weights of the lane's 8 keys under the column's current max, times
+            // 2^kLift1, as fp16: pk[2*c2 + r/2] holds keys r, r+1 of column tile c2.
+            // Column tiles at or past the padded end (last tile only) take an
+            // addend of -inf, i.e. weight 0.
+            uint32_t pk[4];
+            bool cvalid[2];
+#pragma unroll
+            for (int c2 = 0; c2 < 2; ++c2) cvalid[c2] = kbase + 16 * (2 * hf + c2) < a.aligned;
+            auto weights = [&](float mref) {
+#pragma unroll
+              for (int c2 = 0; c2 < 2; ++c2) {
+                const float add = cvalid[c2] ? kLift1 - mref : -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                  const float p0 = fast_exp2(__builtin_fmaf(sc[c2][r], c, add));
+                  const float p1 = fast_exp2(__builtin_fmaf(sc[c2][r + 1], c, add));
+                  pk[2 * c2 + r / 2] = pack_f16(p0, p1);
+                }
+              }
+            };
+            weights(m[k][0]);
+            // A weight above 2^8 (packed: above 2^15; inf and NaN lie higher, and
+            // non-negative fp16 bit patterns order like their values) moves the
+            // columns to their exact running max.
+            const u16x2 pmax = __builtin_elementwise_max(
+                __builtin_elementwise_max(as_u16x2(pk[0]), as_u16x2(pk[1])),
+                __builtin_elementwise_max(as_u16x2(pk[2]), as_u16x2(pk[3])));
+            if (__any(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(pmax, u16x2{0x7800, 0x7800})) != 0u)) {
+              float x = sc[0][0];  // column tile 0 is always valid
+#pragma unroll
+              for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x = cvalid[c2] ? fmaxf(x, sc[c2][r]) : x;
+              x = max_lane_groups(x);
+              const float mn = fmaxf(m[k][0], x * c);
+              const float f = fast_exp2(m[k][0] - mn);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) lsum[k][r] *= f;
+              m[k][0] = mn;
+              weights(mn);
+            }
+            // Column sums on the matrix cores: every row of ones x P is the sum.
+            lsum[k] = mfma16x16x32<UKV_DTYPE_F16>(ones, u32x4{pk[0], pk[1], pk[2], pk[3]}, lsum[k]);
+          }
+          // At most two steps' scores in flight: the next step starts here.
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+
+      // The wave's sums go to its first row tile's slot (TW divides the tiles of a
+      // q head, so a wave's tiles share one head): lanes 32-63 take lanes 0-31 of
+      // colsum[1] (column tiles 2, 3), so lane l holds key l.
+      if constexpr (SCORES) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(colsum[0][0]),
+                                                         __float_as_uint(colsum[1][0]), false, false);
+        if (wv * TW < T) lds.colpart[buf][wv * TW][lane] = __uint_as_float(sw[0]) * kUnlift2;
       }
 
       // Next tile into the other buffer (last read two tiles ago, before the previous barrier).
@@ -325,10 +366,9 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
         // Per (key, head): add the head's runs (fixed order); max over the unit's heads.
         if (hp_pow2 && kSnapTile * a.hp <= (int)blockDim.x) {
           if (tid < kSnapTile * a.hp) {
-            const int key = tid / a.hp, h = tid % a.hp;
+            const int key = tid >> hp_log2, h = tid & (a.hp - 1);
             float x = 0.f;
-            for (int q = h * tph; q < (h + 1) * tph; ++q)
-              if (q == h * tph || q % TW == 0) x += lds.colpart[buf][q][key];
+            for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[buf][q][key];
             for (int o = 1; o < a.hp; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // hp consecutive lanes
             if (h == 0) {
               const int j = kbase + key - key0;
@@ -339,8 +379,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
           float mx = 0.f;
           for (int h = 0; h < a.hp; ++h) {
             float x = 0.f;
-            for (int q = h * tph; q < (h + 1) * tph; ++q)
-              if (q == h * tph || q % TW == 0) x += lds.colpart[buf][q][tid];
+            for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[buf][q][tid];
             mx = fmaxf(mx, x);
           }
           const int j = kbase + tid - key0;
@@ -350,19 +389,14 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
     }
 
     if constexpr (!SCORES) {
-      // Merge the 16 lanes of each row, then write this range's partial (m, l).
+      // This range's partial (m, l) of query row l16 of each tile (lane group 0).
 #pragma unroll
       for (int k = 0; k < TW; ++k) {
         const int tile = wv * TW + k;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float mm = row_max16(m[k][r]);
-          const float ll = row_sum16(lsum[k][r] * fast_exp2(m[k][r] - mm));
-          if (tile < T && l16 == 0) {
-            const int row = tile * 16 + 4 * lg + r;
-            const int64_t grow = (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs;
-            a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(mm, ll);
-          }
+        if (tile < T && lg == 0) {
+          const int row = tile * 16 + l16;
+          const int64_t grow = (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs;
+          a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(m[k][0], lsum[k][0] * (1.f / 128.f));
         }
       }
     }
@@ -486,7 +520,7 @@ size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct SnapPlan {
   bool tiled;
-  int hp, parts, S, Kt, aligned, n_blocks, L_mid;
+  int hp, tw, parts, S, Kt, aligned, n_blocks, L_mid;
   size_t part_off, stats_off, raw_off, total;
 };
 
@@ -497,14 +531,23 @@ SnapPlan snap_plan(int items, int seq_len, int sink, int obs, int num_q_heads, i
   p.aligned = ((std::max(1, p.L_mid) + block_size - 1) / block_size) * block_size;
   p.n_blocks = p.aligned / block_size;
   p.Kt = (p.aligned + kSnapTile - 1) / kSnapTile;
-  // Heads per unit: the largest divisor of n_rep whose rows fit 8 waves x 4 tiles.
+  // Heads per unit: the largest divisor of n_rep whose row tiles fit the waves
+  // with TW tiles each, TW (1, 2 or 4, the smallest that fits) dividing the
+  // tiles of one q head, so that a wave's tiles never span two heads.
   p.hp = 0;
-  for (int h = std::min(n_rep, 32); h >= 1; --h)
-    if (n_rep % h == 0 && h * obs <= 16 * kSnapWaves * kSnapMaxTW) {
-      p.hp = h;
-      break;
+  p.tw = 0;
+  const int tph = obs / 16;
+  if (obs % 16 == 0 && tph > 0)
+    for (int h = std::min(n_rep, 32); h >= 1 && p.hp == 0; --h) {
+      if (n_rep % h != 0) continue;
+      for (int tw = 1; tw <= kSnapMaxTW; tw *= 2)
+        if (tph % tw == 0 && h * tph <= kSnapWaves * tw) {
+          p.hp = h;
+          p.tw = tw;
+          break;
+        }
     }
-  p.tiled = (head_dim == 64 || head_dim == 128) && obs % 16 == 0 && p.hp > 0 && aligned_rows;
+  p.tiled = (head_dim == 64 || head_dim == 128) && p.hp > 0 && aligned_rows;
   p.parts = p.tiled ? n_rep / p.hp : 1;
   if (p.tiled) {
     const int want = (2 * snap_cu_count() + items - 1) / std::max(1, items);
@@ -533,10 +576,9 @@ void launch_tiled(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
 
 template <int DT, int D>
 void launch_tiled_tw(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
-  const int T = a.hp * a.obs / 16;
-  if (T <= kSnapWaves)
+  if (p.tw == 1)
     launch_tiled<DT, D, 1>(a, p, st);
-  else if (T <= 2 * kSnapWaves)
+  else if (p.tw == 2)
     launch_tiled<DT, D, 2>(a, p, st);
   else
     launch_tiled<DT, D, 4>(a, p, st);
@@ -626,7 +668,6 @@ extern "C" int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, co
   a.table = block_table;
   a.max_blocks = max_blocks;
   a.num_pages = num_pages;
-  a.page_size = 16;
   a.layers = layers;
   a.items = items;
   a.sink = sink_len;

@@ -107,6 +107,21 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Two floats -> two packed 16-bit values (round to nearest even).
+__device__ __forceinline__ uint32_t pack_f16(float x0, float x1) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, f16x2));
+}
+__device__ __forceinline__ uint32_t pack_bf16(float x0, float x1) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t w) { return __builtin_bit_cast(u16x2, w); }
+
 // Host side, page_ops.hip: writes row b of k_new/v_new ([batch][num_heads][head_dim],
 // strides new_strides[0..1]) at position lens[b] + pos_offset of sequence b (page
 // block_table[b][pos / block_size], slot pos % block_size); positions outside the table
