@@ -142,6 +142,10 @@ DENSE_CASES = [
     (8, 4, 128, 1100, 64, 128),       # tiled, 4 row tiles per wave (512 rows)
     (2, 8, 128, 700, 16, 128),        # tiled, heads split into 2 units per group
     (4, 4, 64, 500, 16, 32),          # tiled, D=64
+    (4, 4, 128, 900, 32, 48),         # tiled, 3 tiles per head: 1 row tile per wave, 2 heads per unit
+    (2, 4, 64, 777, 16, 80),          # tiled, 5 tiles per head: 1 row tile per wave, 1 head per unit
+    (2, 4, 128, 1234, 0, 96),         # tiled, 6 tiles per head: 2 row tiles per wave, 2 heads per unit
+    (2, 8, 128, 640, 16, 16),         # tiled, 1 tile per head: 8 heads per unit
     (8, 4, 32, 2795, 16, 16),         # scalar (D=32): the reference's block-alignment test shape
     (2, 2, 64, 300, 8, 24),           # scalar (obs not a multiple of 16)
     (4, 2, 128, 64 + 64 + 16, 64, 64),  # N = 1
