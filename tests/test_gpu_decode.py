@@ -9,7 +9,9 @@ same bound on the small cases.
 Full-size configs 2 and 3 are checked on sampled sequences (their pages are
 gathered into a compact pool and the oracle runs on that), plus two
 size-independent properties: bit-identical output under a random permutation of
-the physical pages, and run-to-run determinism.
+the physical pages, and run-to-run determinism. Closed forms: one attended token
+returns its V row bit for bit, equal keys return the mean of V, and extra table
+columns change nothing (bit-identical).
 """
 import math
 
@@ -171,6 +173,41 @@ def test_nan_in_unused_slots_does_not_leak(cuda):
     out = to_f32(decode_gpu(workloads.to_torch(case)))
     assert np.isfinite(out).all()
     assert_close(out, expected_dense(case), "NaN rows past the length")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_closed_form_invariants(cuda, dtype):
+    # One attended token: the output is that token's V row, bit for bit.
+    case = custom_case(31, 4, 32, 8, 128, [1, 1, 1, 1], dtype=dtype)
+    out = decode_gpu(workloads.to_torch(case)).view(_torch().int16).cpu().numpy().view(np.uint16)
+    for b in range(4):
+        page = case["block_table"][b, 0]
+        for h in range(32):
+            assert np.array_equal(out[b, h], case["v_cache"][page, 0, h // 4]), (b, h)
+    # Every key of a head equal: uniform weights, the output is the mean of the head's V rows.
+    lens = [300, 17, 1024]
+    case = custom_case(32, 3, 32, 8, 128, lens, dtype=dtype)
+    case["k_cache"] = case["k_cache"].copy()
+    case["k_cache"][:, :] = case["k_cache"][0, 0]
+    got = to_f32(decode_gpu(workloads.to_torch(case)))
+    v = oracle.bits_to_f32(case["v_cache"], workloads.DTYPE_CODES[dtype]).astype(np.float64)
+    for b, L in enumerate(lens):
+        rows = np.concatenate([v[case["block_table"][b, p]] for p in range((L + 15) // 16)])[:L]  # [L, Hkv, D]
+        mean = rows.mean(axis=0)
+        for h in range(32):
+            assert np.all(np.abs(got[b, h] - mean[h // 4]) <= ATOL + RTOL * np.abs(mean[h // 4])), (b, h)
+    # Extra table columns holding other pages change nothing (bit-identical). The batch is
+    # long enough (3 x 688 pages) that both tables split over one workgroup per CU.
+    lens = [200, 33, 11000]
+    case = custom_case(33, 3, 32, 8, 128, lens, dtype=dtype)
+    base = decode_gpu(workloads.to_torch(case)).view(_torch().int16).cpu().numpy()
+    wide = case["block_table"]
+    extra = np.random.default_rng(5).integers(0, case["N"], size=(3, 9)).astype(np.int32)
+    case["block_table"] = np.concatenate([wide, extra], axis=1)
+    for b, L in enumerate(lens):  # and past each sequence's pages within its row
+        case["block_table"][b, (L + 15) // 16:wide.shape[1]] = extra[b, 0]
+    again = decode_gpu(workloads.to_torch(case)).view(_torch().int16).cpu().numpy()
+    assert np.array_equal(base, again)
 
 
 def test_explicit_n_rep_and_scale(cuda):
