@@ -155,6 +155,10 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
   const int hp_log2 = 31 - __builtin_clz(a.hp);
   const int item_b = item / a.layers, item_l = item - item_b * a.layers;  // sequence, layer
   const int32_t* trow = a.table ? a.table + (int64_t)item_b * a.max_blocks : nullptr;
+  // The kernel never writes the table: read it through the constant address space, so that
+  // wave-uniform ids come through the scalar cache.
+  typedef const __attribute__((address_space(4))) int32_t cint32;
+  cint32* trow_c = (cint32*)trow;
   // MFMA A operands of the column sums (fp16 1.0 pairs): all ones (pass 1), and
   // rows 0 and 4 selecting dwords 0-1 and 2-3 of the B operand (pass 2).
   constexpr uint32_t kOnes = 0x3C003C00u;
@@ -204,20 +208,38 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
     // key_row() with the item's and the unit's terms taken out of the tile loop.
     const uint16_t* kg = a.k + (int64_t)item_l * a.k_sl + (int64_t)g * a.k_sh;
     u32x4 pre[CPT];
+    // Per chunk, the thread's key offset in a tile, its token's slot in a page and its
+    // page relative to the wave's first page are the same for every tile (a tile is 64
+    // keys = 4 pages), so only the wave-uniform page ids change from tile to tile.
+    int64_t roff[CPT];  // element offset of the chunk within its page (paged) or tile (dense)
+    bool second[CPT];   // paged: the chunk's key is on the wave's second page
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int cc = tid + i * 64 * kSnapWaves;
+      const int kk = cc / (D / 8), kk0 = __builtin_amdgcn_readfirstlane(kk);
+      const int t = a.sink + kk;  // token of the key in tile 0 (tile u adds 64u = 4u pages)
+      second[i] = (t >> 4) != ((a.sink + kk0) >> 4);
+      roff[i] = (trow ? (int64_t)(t & 15) * a.k_st : (int64_t)t * a.k_st) + 8 * (cc % (D / 8));
+    }
     auto fetch = [&](int tile_idx) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int cc = tid + i * 64 * kSnapWaves;
         const int j = tile_idx * kSnapTile + cc / (D / 8);  // mid key
-        const int t = a.sink + j;
         const uint16_t* src = nullptr;
         if (trow) {
-          const int page = j < a.L_mid && (t >> 4) < a.max_blocks ? trow[t >> 4] : -1;
-          if ((unsigned)page < (unsigned)a.num_pages) src = kg + (int64_t)page * a.k_sb + (int64_t)(t & 15) * a.k_st;
+          // A wave's keys (64 / (D/8) <= 8 consecutive ones) lie in at most two pages:
+          // their ids are read once per wave through the scalar cache.
+          const int blk_a = (a.sink + __builtin_amdgcn_readfirstlane(j)) >> 4;
+          const int id_a = blk_a < a.max_blocks ? trow_c[blk_a] : -1;
+          const int id_b = blk_a + 1 < a.max_blocks ? trow_c[blk_a + 1] : -1;
+          const int page = second[i] ? id_b : id_a;
+          if (j < a.L_mid && (unsigned)page < (unsigned)a.num_pages)
+            src = kg + (int64_t)page * a.k_sb + roff[i];
         } else if (j < a.L_mid) {
-          src = kg + (int64_t)item_b * a.k_sb + (int64_t)t * a.k_st;
+          src = kg + (int64_t)item_b * a.k_sb + (int64_t)tile_idx * kSnapTile * a.k_st + roff[i];
         }
-        pre[i] = src ? ld16(src + 8 * (cc % (D / 8))) : u32x4{0u, 0u, 0u, 0u};
+        pre[i] = src ? ld16(src) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto stash = [&](int buf) {
