@@ -250,6 +250,29 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
       }
     };
 
+    // Per (key, head) of tile `tile`: add the head's waves' column sums (fixed order),
+    // take the max over the unit's heads, and fold it into the range's running max.
+    auto head_sum = [&](int tile, int b) {
+      const int kb0 = tile * kSnapTile - key0;
+      if (hp_pow2 && kSnapTile * a.hp <= (int)blockDim.x) {
+        if (tid < kSnapTile * a.hp) {
+          const int key = tid >> hp_log2, h = tid & (a.hp - 1);
+          float x = 0.f;
+          for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[b][q][key];
+          for (int o = 1; o < a.hp; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // hp consecutive lanes
+          if (h == 0) lds.colmax[kb0 + key] = fmaxf(lds.colmax[kb0 + key], x);
+        }
+      } else if (tid < kSnapTile) {
+        float mx = 0.f;
+        for (int h = 0; h < a.hp; ++h) {
+          float x = 0.f;
+          for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[b][q][tid];
+          mx = fmaxf(mx, x);
+        }
+        lds.colmax[kb0 + tid] = fmaxf(lds.colmax[kb0 + tid], mx);
+      }
+    };
+
     __syncthreads();  // the previous unit is done with both buffers
     fetch(t0);
     stash(0);
@@ -303,6 +326,11 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
             if ((j + 1) % TW == 0) load_half((j + 1) / TW);
             scores(j + 1, acc[(j + 1) & 1]);
           }
+          // The previous tile's head sums (its column sums were written before the last
+          // barrier; that buffer is written again only after the next one), while the
+          // scores above run on the matrix cores.
+          if constexpr (SCORES)
+            if (j == 0 && ti > t0) head_sum(ti - 1, buf ^ 1);
           f32x4(&sc)[2] = acc[j & 1];
           if constexpr (SCORES) {
             // Weights times 2^kLift2 as fp16, dword 2*c2 + r/2 = rows r, r+1 of
@@ -384,31 +412,9 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
       __syncthreads();  // tile ti+1 and this tile's column sums are visible
       if (ti + 2 < t1) fetch(ti + 2);
 
-      if constexpr (SCORES) {
-        // Per (key, head): add the head's runs (fixed order); max over the unit's heads.
-        if (hp_pow2 && kSnapTile * a.hp <= (int)blockDim.x) {
-          if (tid < kSnapTile * a.hp) {
-            const int key = tid >> hp_log2, h = tid & (a.hp - 1);
-            float x = 0.f;
-            for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[buf][q][key];
-            for (int o = 1; o < a.hp; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // hp consecutive lanes
-            if (h == 0) {
-              const int j = kbase + key - key0;
-              lds.colmax[j] = fmaxf(lds.colmax[j], x);
-            }
-          }
-        } else if (tid < kSnapTile) {
-          float mx = 0.f;
-          for (int h = 0; h < a.hp; ++h) {
-            float x = 0.f;
-            for (int q = h * tph; q < (h + 1) * tph; q += TW) x += lds.colpart[buf][q][tid];
-            mx = fmaxf(mx, x);
-          }
-          const int j = kbase + tid - key0;
-          lds.colmax[j] = fmaxf(lds.colmax[j], mx);
-        }
-      }
     }
+    // The tile loop's last column sums (visible after its last barrier).
+    if constexpr (SCORES) head_sum(t1 - 1, (t1 - 1 - t0) & 1);
 
     if constexpr (!SCORES) {
       // This range's partial (m, l) of query row l16 of each tile (lane group 0).
