@@ -728,8 +728,13 @@ extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void*
   a.scale = softmax_scale;
   a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+  // The tiled kernel keeps a row's offset within its page in 32 bits.
+  auto in_page_ok = [&](int64_t st, int64_t sh) {
+    return st >= 0 && sh >= 0 && 15 * st + (int64_t)(num_kv_heads - 1) * sh + head_dim <= (int64_t)UINT32_MAX;
+  };
   const bool strides_ok = mul8(a.q_st) && mul8(a.q_sh) && mul8(a.k_sp) && mul8(a.k_st) && mul8(a.k_sh) &&
-                          mul8(a.v_sp) && mul8(a.v_st) && mul8(a.v_sh);
+                          mul8(a.v_sp) && mul8(a.v_st) && mul8(a.v_sh) && in_page_ok(a.k_st, a.k_sh) &&
+                          in_page_ok(a.v_st, a.v_sh);
   const bool fast = head_dim == 128 && softmax_scale > 0.f && std::isfinite(softmax_scale) && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
                     strides_ok && al16(q) && al16(out) && al16(k_cache) && al16(v_cache) && max_blocks > 0;
   if (fast) {
