@@ -473,13 +473,15 @@ __device__ __forceinline__ float block_reduce_256(float x, float* red, bool is_m
 // Merges the partials of one (sequence, q head): log-sum-exp in log2 units.
 // The sequence's pages [S, S+n) of the batch's P pages were split over
 // workgroups w = floor(((S+1)G - 1)/P) .. floor(((S+n)G - 1)/P), whose partials
-// sit in slots w + b. 256 threads: the weights are computed once into LDS, then
-// thread (cs, dq) sums float4 dims 4*dq.. over partials cs, cs+CS, ... with
-// coalesced row reads, and the CS partial sums meet in LDS.
+// sit in slots w + b. 256 threads: thread (cs, dq) owns float4 dims 4*dq.. of
+// partials cs, cs+CS, ...; it issues the loads of its first kPre rows together
+// with the (m, l) loads, so that one memory round trip serves both; the weights
+// are computed once into LDS, and the CS partial sums meet in LDS.
 template <int DT, int D>
 __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a) {
   constexpr int TD = D / 4;       // threads per partial row (float4 each)
   constexpr int CS = 256 / TD;    // chunk groups
+  constexpr int kPre = 4;         // partial rows per thread loaded before the weights
   extern __shared__ float w_s[];  // [grid_wgs] weights, then [CS][D] sums
   __shared__ float red[4];
 
@@ -501,30 +503,48 @@ __global__ void __launch_bounds__(256) page16_combine_kernel(const DecodeArgs a)
     return ((w + 1) * P) / G > (w * P) / G;
   };
 
-  float mx = -INFINITY;
-  for (int c = tid; c < n_chunks; c += 256)
+  const int cs = tid / TD;
+  const int dq = tid % TD;
+  const float* po = a.part_o + base * D + 4 * dq;
+  const int64_t cstride = (int64_t)a.Hq * D;
+  f32x4 rows[kPre];  // partials cs + k*CS (in the workspace even when stale; skipped below)
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    const int c = cs + k * CS;
+    rows[k] = c < n_chunks ? *reinterpret_cast<const f32x4*>(po + (int64_t)c * cstride) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const bool own0 = tid < n_chunks && owns_pages(tid);
+  const float2 ml0 = own0 ? a.part_ml[base + (int64_t)tid * a.Hq] : make_float2(-INFINITY, 0.f);
+
+  float mx = ml0.x;
+  for (int c = tid + 256; c < n_chunks; c += 256)
     if (owns_pages(c)) mx = fmaxf(mx, a.part_ml[base + (int64_t)c * a.Hq].x);
   const float M = block_reduce_256(mx, red, true);
   float dsum = 0.f;
   for (int c = tid; c < n_chunks; c += 256) {
-    if (!owns_pages(c)) {
+    const bool own = c == tid ? own0 : owns_pages(c);
+    if (!own) {
       w_s[c] = -1.f;  // marks an empty slot (real weights are >= 0 or NaN)
       continue;
     }
-    const float2 ml = a.part_ml[base + (int64_t)c * a.Hq];
+    const float2 ml = c == tid ? ml0 : a.part_ml[base + (int64_t)c * a.Hq];
     const float w = exp2f(ml.x - M);
     w_s[c] = w;
     dsum += ml.y * w;
   }
   const float den = block_reduce_256(dsum, red, false);  // also orders the w_s writes
 
-  const int cs = tid / TD;
-  const int dq = tid % TD;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const float* po = a.part_o + base * D + 4 * dq;
-  const int64_t cstride = (int64_t)a.Hq * D;
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    const int c = cs + k * CS;
+    if (c < n_chunks) {
+      const float w = w_s[c];
+      if (!(w < 0.f)) acc += w * rows[k];
+    }
+  }
 #pragma unroll 4
-  for (int c = cs; c < n_chunks; c += CS) {
+  for (int c = cs + kPre * CS; c < n_chunks; c += CS) {
     const float w = w_s[c];
     if (!(w < 0.f)) acc += w * *reinterpret_cast<const f32x4*>(po + (int64_t)c * cstride);
   }
