@@ -354,3 +354,53 @@ def test_exhaustion_keeps_earlier_pages_in_the_device_table(cuda):
     assert batch.page_lists == [[0, 2], [1]]
     assert batch.block_table[:, :2].cpu().tolist() == [[0, 2], [1, 0]]
     assert batch.seq_lens == [16, 16] and batch.cache_seqlens.cpu().tolist() == [16, 16]
+
+
+@pytest.mark.gpu
+def test_layer_calls_replay_from_a_captured_graph(cuda):
+    # The per-layer fused append + decode calls of a step hold no host synchronisation and
+    # no memset, so a serving loop can capture them. Capture one step's layers, then replay
+    # the graph several times with eager work in between: every replay must equal the eager
+    # result bit for bit (the appends rewrite the same rows with the same values).
+    from unifiedkv_amd.decode_step import DecodeBatch
+
+    rng = np.random.default_rng(21)
+    n_layers, Hq, Hkv, D, N, dtype = 3, 32, 8, 128, 96, "bf16"
+    lens0 = [40, 16, 100, 5]
+    B = len(lens0)
+    pool = PagedKVPool(16, n_layers, Hkv, D, _tdt(dtype), num_blocks=N, device=cuda)
+    pool.k_cache.copy_(_dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda))
+    pool.v_cache.copy_(_dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda))
+    lists = [pool.allocate_blocks(max(1, -(-L // 16))) for L in lens0]
+    batch = DecodeBatch(pool, lists, lens0)
+    scale = 1.0 / math.sqrt(D)
+    ins = [tuple(_dev(_rand_bits(rng, shape, dtype), dtype, cuda) for shape in ((B, Hq, D), (B, Hkv, D), (B, Hkv, D)))
+           for _ in range(n_layers)]
+    batch.begin_step()
+    eager = [batch.attention(layer, *ins[layer], softmax_scale=scale, n_rep=Hq // Hkv).clone()
+             for layer in range(n_layers)]
+    torch.cuda.synchronize()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the allocator on the capture stream
+        for layer in range(n_layers):
+            batch.attention(layer, *ins[layer], softmax_scale=scale, n_rep=Hq // Hkv)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [batch.attention(layer, *ins[layer], softmax_scale=scale, n_rep=Hq // Hkv)
+                for layer in range(n_layers)]
+    for rep in range(4):
+        for o in outs:
+            o.fill_(0)
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(n_layers):
+            assert torch.equal(outs[layer].view(torch.int16), eager[layer].view(torch.int16)), (rep, layer)
+        # eager work of the program between replays
+        again = batch.attention(1, *ins[1], softmax_scale=scale, n_rep=Hq // Hkv)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), eager[1].view(torch.int16))
+    batch.end_step()
