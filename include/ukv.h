@@ -241,7 +241,8 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  *   raw[n] = sum of s over keys [block_size * n, block_size * (n + 1));
  *   scores[item * scores_stride + n] = max(raw[n-1], raw[n], raw[n+1]) if N >= 3, else raw[n]
  * for n < N = ukv_snapkv_block_count(...), which is 0 (nothing written, UKV_OK) when
- * L < sink_len + obs_len + block_size. fp32 arithmetic from 16-bit inputs.
+ * L < sink_len + obs_len + block_size. Scores, maxima and sums are fp32 from 16-bit inputs; each
+ * softmax weight is rounded to fp16 (relative error <= 2^-11) where the matrix cores sum it.
  *   q_obs        [items, num_q_heads, obs_len, head_dim], element strides q_strides[0..2]
  *                {item, head, query}, last dimension contiguous
  *   k            K rows with element strides k_strides[0..3] = {layer, seq-or-page, token, head}:
@@ -252,8 +253,8 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  *                outside [0, num_pages) read as zero rows
  * num_q_heads must equal num_kv_heads * n_rep (q head h reads KV head h / n_rep); block_size must
  * be 16 (the page size; the reference's SnapKV block); layers * seqs <= 65535; otherwise
- * UKV_ERR_INVALID_ARGUMENT. The workspace (ukv_snapkv_workspace_bytes) needs no initialisation. Replaces core/scheduler.py:565-592 and the
- * scoring steps of core/compress.py:116-130.
+ * UKV_ERR_INVALID_ARGUMENT. The workspace (ukv_snapkv_workspace_bytes) needs no initialisation.
+ * Replaces core/scheduler.py:565-592 and the scoring steps of core/compress.py:116-130.
  */
 int ukv_snapkv_block_count(int seq_len, int sink_len, int obs_len, int block_size);
 size_t ukv_snapkv_workspace_bytes(int layers, int seqs, int seq_len, int sink_len, int obs_len, int num_q_heads,
