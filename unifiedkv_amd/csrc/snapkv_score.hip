@@ -175,8 +175,8 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
 
     // This wave's row tiles: w*TW .. w*TW+TW-1 (tiles past T are zero and unused).
     u32x4 qa[TW][STEPS];
-    // pass 1: m[k][0] is the running max (log2 units) of query column l16 of
-    //         tile k, the same in the 4 lane groups, and every row of lsum[k]
+    // pass 1: m[k][0] is kLift1 minus the running max (log2 units) of query column
+    //         l16 of tile k, the same in the 4 lane groups, and every row of lsum[k]
     //         holds 2^kLift1 times the column's running sum of weights;
     // pass 2: m[k][r] = m' - kLift2 of query row 4*lg + r of tile k.
     float m[TW][4];
@@ -193,7 +193,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
       for (int st = 0; st < STEPS; ++st) qa[k][st] = on ? ld16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        m[k][r] = SCORES ? INFINITY : -INFINITY;  // pass 2: rows past the unit weigh 0
+        m[k][r] = INFINITY;  // pass 1: kLift1 - max with max = -inf; pass 2: rows past the unit weigh 0
         if constexpr (SCORES) {
           if (on) {  // C rows 4*lg + r of the tile
             const int row = tile * 16 + 4 * lg + r;
@@ -357,10 +357,10 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
             bool cvalid[2];
 #pragma unroll
             for (int c2 = 0; c2 < 2; ++c2) cvalid[c2] = kbase + 16 * (2 * hf + c2) < a.aligned;
-            auto weights = [&](float mref) {
+            auto weights = [&](float nref) {  // nref = kLift1 - the column's max
 #pragma unroll
               for (int c2 = 0; c2 < 2; ++c2) {
-                const float add = cvalid[c2] ? kLift1 - mref : -INFINITY;
+                const float add = cvalid[c2] ? nref : -INFINITY;
 #pragma unroll
                 for (int r = 0; r < 4; r += 2) {
                   const float p0 = fast_exp2(__builtin_fmaf(sc[c2][r], c, add));
@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
                 }
               }
             };
-            weights(m[k][0]);
+            weights(m[k][0]);  // pass 1 keeps kLift1 - max here
             // A weight above 2^8 (packed: above 2^15; inf and NaN lie higher, and
             // non-negative fp16 bit patterns order like their values) moves the
             // columns to their exact running max.
@@ -383,12 +383,13 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
 #pragma unroll
                 for (int r = 0; r < 4; ++r) x = cvalid[c2] ? fmaxf(x, sc[c2][r]) : x;
               x = max_lane_groups(x);
-              const float mn = fmaxf(m[k][0], x * c);
-              const float f = fast_exp2(m[k][0] - mn);
+              const float mo = kLift1 - m[k][0];
+              const float mn = fmaxf(mo, x * c);
+              const float f = fast_exp2(mo - mn);
 #pragma unroll
               for (int r = 0; r < 4; ++r) lsum[k][r] *= f;
-              m[k][0] = mn;
-              weights(mn);
+              m[k][0] = kLift1 - mn;
+              weights(m[k][0]);
             }
             // Column sums on the matrix cores: every row of ones x P is the sum.
             lsum[k] = mfma16x16x32<UKV_DTYPE_F16>(ones, u32x4{pk[0], pk[1], pk[2], pk[3]}, lsum[k]);
@@ -424,7 +425,8 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
         if (tile < T && lg == 0) {
           const int row = tile * 16 + l16;
           const int64_t grow = (int64_t)(h0 + row / a.obs) * a.obs + row % a.obs;
-          a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] = make_float2(m[k][0], lsum[k][0] * (1.f / 128.f));
+          a.part_stats[((int64_t)item * a.S + s) * rows_all + grow] =
+              make_float2(kLift1 - m[k][0], lsum[k][0] * (1.f / 128.f));
         }
       }
     }
