@@ -116,6 +116,11 @@ int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
  * seqlens[b] - 1 unless seqlens[b] <= 0, the position is beyond max_blocks * 16 or its page
  * id is outside [0, num_pages). The split kernel writes the rows itself while it reads that
  * page (one launch fewer per layer); shapes it does not take run the append kernel first.
+ * Precondition of the fused form: no page that one sequence attends is the page another
+ * sequence's token is written to. The pool gives every sequence pages of its own, so this
+ * holds unless a length exceeds its table row (then its zero padding, page 0, is attended;
+ * the reference's index_put rejects such a length). Where it fails, that page's read races
+ * with the write: call ukv_kv_append, then ukv_page16_decode.
  * Workspace as for ukv_page16_decode. Replaces core/scheduler.py:401-418 (block_pos / tok_pos,
  * the K and V index_put, attn_lens = old_lens + 1, page16_decode_attention).
  */

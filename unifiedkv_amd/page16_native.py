@@ -156,7 +156,10 @@ def page16_decode_append_attention(
     (or [batch, 1, num_kv_heads, head_dim]) rows, written to position
     cache_seqlens[b] - 1 of sequence b before it is attended. Same result and pool
     contents as core/scheduler.py:401-418 (block_pos / tok_pos, the two
-    ``index_put_``, ``attn_lens = old_lens + 1``, ``page16_decode_attention``).
+    ``index_put_``, ``attn_lens = old_lens + 1``, ``page16_decode_attention``),
+    provided no page one sequence attends is another sequence's append target
+    (true for the pool's per-sequence pages; a length beyond its table row
+    attends the zero padding, page 0, and the reference rejects such a length).
     """
     q, block_table, cache_seqlens, batch, num_q_heads, num_kv_heads, head_dim, dev = _prepare(
         q, k_cache, v_cache, block_table, cache_seqlens)
