@@ -196,9 +196,9 @@ int ukv_decode_prologue(int32_t* block_table, int max_blocks, int batch, const i
 
 /*
  * Retain-set selection: for each row r, the k_r indices i < n_r with the largest scores
- * (float32 scores[r * row_stride + i]), ties to the lower index, NaN ranked above every
- * number, written to out[r * out_stride + 0 .. k_r-1] in ascending order; the remaining
- * entries up to k_max are set to -1. row_n / row_k are optional int32 [rows] device arrays
+ * (float32 scores[r * row_stride + i]), ties (-0 and +0 are equal) to the lower index, NaN
+ * ranked above every number, written to out[r * out_stride + 0 .. k_r-1] in ascending order;
+ * the remaining entries up to k_max are set to -1. row_n / row_k are optional int32 [rows] device arrays
  * (NULL: n_max / k_max for every row); k_r is clamped to [0, min(n_r, k_max)].
  * Replaces torch.topk + sort of core/scheduler.py:613-616 and core/compress.py:141-142, whose
  * order of equal scores is unspecified.

@@ -59,7 +59,8 @@ def select_topk(scores: np.ndarray, k: int) -> np.ndarray:
     out = np.empty((scores.shape[0], k), dtype=np.int32)
     for r, row in enumerate(scores):
         idx = np.arange(row.shape[0])
-        key = np.where(np.isnan(row), np.inf, row.astype(np.float64))
+        with np.errstate(invalid="ignore"):  # signalling-NaN payloads warn on the widening cast
+            key = np.where(np.isnan(row), np.inf, row.astype(np.float64))
         nan_first = np.isnan(row)
         order = np.lexsort((idx, -key, ~nan_first))  # NaN first, then score desc, then index asc
         out[r] = np.sort(order[:k])

@@ -20,6 +20,7 @@ namespace ukv {
 __device__ __forceinline__ uint64_t select_key(float s, int idx) {
   uint32_t u = __float_as_uint(s);
   if (s != s) u = 0x7fc00000u;  // canonical NaN ranks highest
+  if (u == 0x80000000u) u = 0u;  // -0 equals +0: the tie goes to the lower index
   const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // ascending with the float value
   return (uint64_t(~ord) << 32) | uint32_t(idx);
 }
