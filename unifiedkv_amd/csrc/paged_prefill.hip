@@ -112,7 +112,7 @@ constexpr int kTileKeys = 32;
 constexpr int kRowPad = UKV_PREFILL_KPAD;
 constexpr int kVRowPad = UKV_PREFILL_VPAD;
 constexpr int kStages = 3;
-constexpr int kColBlocks = 2;  // 16-column blocks per wave
+constexpr int kColBlocks = 3;  // 16-column blocks per wave (3 measured 2.5 % faster than 2; 247 VGPRs)
 
 // Fallback for a workgroup whose key range holds a bf16 V value of magnitude
 // >= 65520 (or infinite), which fp16 cannot carry: every (query, head) pair
