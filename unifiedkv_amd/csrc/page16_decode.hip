@@ -29,6 +29,7 @@
 // serves shapes the split kernel is not instantiated for (head_dim not in
 // {64, 128, 256}, n_rep > 16, or rows not 16-byte aligned).
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -619,15 +620,30 @@ namespace {
 
 constexpr int kMinPagesPerWg = 8;  // below this a workgroup's setup outweighs its pages
 
+// CU count of the current device, cached per device id (0 = not yet read; a
+// racing first read stores the same value twice).
 int device_cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (dev < 64) cached[dev] = cus;
+  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
+}
+
+// UKV_PAGE16_WGS, read once per process (0 when unset or not a positive number).
+int env_wgs() {
+  static const int v = [] {
+    const char* env = std::getenv("UKV_PAGE16_WGS");
+    const int x = (env && *env) ? std::atoi(env) : 0;
+    return x > 0 ? std::min(x, 65535) : 0;
+  }();
+  return v;
 }
 
 // Workgroups G sharing the batch's pages: one per CU (a single round of equal
@@ -635,11 +651,7 @@ int device_cu_count() {
 // (batch * max_blocks pages) gives each fewer than kMinPagesPerWg pages;
 // UKV_PAGE16_WGS overrides it for launch-shape sweeps.
 int split_wgs_for(int batch, int max_blocks) {
-  const char* env = std::getenv("UKV_PAGE16_WGS");
-  if (env && *env) {
-    const int v = std::atoi(env);
-    if (v > 0) return std::min(v, 65535);
-  }
+  if (const int v = env_wgs()) return v;
   const long long bound = (long long)batch * (long long)std::max(max_blocks, 1);
   const long long g = std::min<long long>(device_cu_count(), (bound + kMinPagesPerWg - 1) / kMinPagesPerWg);
   return (int)std::max<long long>(1, g);
