@@ -12,12 +12,18 @@ in float64 on host arrays:
 * ``maxpool3``            torch.nn.functional.max_pool1d(kernel_size=3, stride=1, padding=1)
 * ``score_heads_f32``     the dense fp32 formulation (matmul, softmax, mean) for a subset of heads:
                           the CPU baseline's sample
+* ``score_layer_blocks_model_dtype``  the same steps with the reference's rounding points: every
+                          torch op of :586-588 runs in the model dtype there, so its output is
+                          rounded to bf16 / fp16 (matmul, * scale, softmax, mean, block sum);
+                          bounds how far exact scores sit from the reference's own arithmetic
 """
 from __future__ import annotations
 
 import math
 
 import numpy as np
+
+from . import oracle as _bits
 
 
 def mid_keys(K: np.ndarray, sink_len: int, obs_len: int, block_size: int):
@@ -60,6 +66,45 @@ def score_layer_blocks(K, Q_obs, *, sink_len: int, obs_len: int, n_rep: int, blo
     A /= A.sum(axis=-1, keepdims=True)
     s = A.mean(axis=1).max(axis=0)                      # [aligned]
     blocks = s.reshape(N, block_size).sum(axis=-1)
+    return maxpool3(blocks) if N >= 3 else blocks
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Values of x rounded to "bf16" or "fp16" (nearest-even, via fp32), returned as float64."""
+    x32 = np.asarray(x, dtype=np.float32)
+    if dtype == "bf16":
+        r = _bits.bf16_bits_to_f32(_bits.f32_to_bf16_bits(x32))
+    elif dtype == "fp16":
+        r = x32.astype(np.float16).astype(np.float32)
+    elif dtype == "exact":
+        return np.asarray(x, dtype=np.float64)
+    else:
+        raise ValueError(dtype)
+    return r.astype(np.float64)
+
+
+def score_layer_blocks_model_dtype(K, Q_obs, *, sink_len: int, obs_len: int, n_rep: int, dtype: str,
+                                   block_size: int = 16, scale: float = None) -> np.ndarray:
+    """core/scheduler.py:583-591 with each torch op's output rounded to the model dtype.
+
+    torch computes matmul, softmax, mean and sum in fp32 internally and rounds their outputs
+    to the tensor dtype; ``* scale`` rounds too; max and max_pool1d are exact. dtype "exact"
+    reduces this to score_layer_blocks.
+    """
+    K = np.asarray(K, dtype=np.float64)
+    Q = np.asarray(Q_obs, dtype=np.float64)
+    scale = K.shape[2] ** -0.5 if scale is None else scale
+    K_mid, N = mid_keys(K, sink_len, obs_len, block_size)
+    if N == 0:
+        return np.empty(0)
+    Ke = repeat_kv(K_mid, n_rep)
+    S = round_to(np.matmul(Q, Ke.transpose(0, 2, 1)), dtype)
+    S = round_to(S * scale, dtype)
+    S = S - S.max(axis=-1, keepdims=True)
+    A = np.exp(S)
+    A = round_to(A / A.sum(axis=-1, keepdims=True), dtype)
+    s = round_to(A.mean(axis=1), dtype).max(axis=0)
+    blocks = round_to(s.reshape(N, block_size).sum(axis=-1), dtype)
     return maxpool3(blocks) if N >= 3 else blocks
 
 

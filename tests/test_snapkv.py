@@ -33,6 +33,50 @@ def test_loops_equal_vectorised_on_tiny_shapes():
         assert a.shape == b.shape and np.allclose(a, b, rtol=1e-12, atol=1e-15)
 
 
+MODEL_DTYPE_CASES = [(2, 4, 64, 600, 16, 32), (4, 2, 128, 1000, 64, 64), (1, 8, 128, 333, 4, 16)]
+
+
+def _model_dtype_inputs(rng, case, dtype):
+    h_kv, n_rep, D, L, sink, obs = case
+    code = workloads.DTYPE_CODES[dtype]
+    K = dec_oracle.bits_to_f32(_bits(rng, (h_kv, L, D), dtype), code)
+    Q = dec_oracle.bits_to_f32(_bits(rng, (h_kv * n_rep, obs, D), dtype), code)
+    return K, Q
+
+
+def test_model_dtype_exact_mode_is_the_fp64_oracle():
+    rng = np.random.default_rng(1)
+    K, Q = rng.standard_normal((2, 300, 64)), rng.standard_normal((8, 32, 64))
+    a = so.score_layer_blocks(K, Q, sink_len=16, obs_len=32, n_rep=4)
+    b = so.score_layer_blocks_model_dtype(K, Q, sink_len=16, obs_len=32, n_rep=4, dtype="exact")
+    np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("case", MODEL_DTYPE_CASES)
+def test_model_dtype_rounding_matches_torch_cpu_kernels(dtype, case):
+    """torch's own CPU kernels running core/scheduler.py:583-591's op sequence in the model dtype
+    (an implementation independent of the numpy emulation) give the same block scores."""
+    import torch
+
+    h_kv, n_rep, D, L, sink, obs = case
+    rng = np.random.default_rng(L + D)
+    K, Q = _model_dtype_inputs(rng, case, dtype)
+    emu = so.score_layer_blocks_model_dtype(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep, dtype=dtype)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    Kt, Qt = torch.tensor(K, dtype=tdt), torch.tensor(Q, dtype=tdt)
+    Km = Kt[:, sink:L - obs, :]
+    aligned = math.ceil(Km.shape[1] / 16) * 16
+    Km = torch.nn.functional.pad(Km, (0, 0, 0, aligned - Km.shape[1]))
+    Ke = Km.repeat_interleave(n_rep, dim=0)
+    attn = torch.softmax(torch.matmul(Qt, Ke.transpose(-2, -1)) * (D ** -0.5), dim=-1)
+    blocks = attn.mean(dim=1).max(dim=0).values.view(aligned // 16, 16).sum(dim=-1).float()
+    ref = torch.nn.functional.max_pool1d(blocks.view(1, 1, -1), kernel_size=3, stride=1, padding=1).view(-1)
+    np.testing.assert_allclose(emu, ref.numpy().astype(np.float64), rtol=2.0 ** -10, atol=0)
+    exact = so.score_layer_blocks(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep)
+    assert np.max(np.abs(emu - exact) / exact) < 2.0 ** -6  # the model dtype's own rounding stays small
+
+
 def test_maxpool_definition():
     assert so.maxpool3(np.array([1.0, 5.0, 2.0, 0.0, 3.0])).tolist() == [5.0, 5.0, 5.0, 3.0, 3.0]
     assert so.maxpool3(np.array([2.0, 1.0, 0.5])).tolist() == [2.0, 2.0, 1.0]
@@ -239,3 +283,29 @@ def test_config5_shape_sampled_items(cuda):
         dense = pool[l][perm[b].long().cuda()].reshape(pages * 16, h_kv, D).transpose(0, 1).float().cpu().numpy()
         want = so.score_layer_blocks(dense, q[b, l].float().cpu().numpy(), sink_len=sink, obs_len=obs, n_rep=n_rep)
         _assert_scores(got[b * layers + l], want, f"config-5 item seq {b} layer {l}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_scores_and_selection_against_the_reference_dtype_arithmetic(cuda, dtype):
+    """The kernel computes exact fp32 scores; the reference rounds every step to the model dtype
+    (core/scheduler.py:586-588). Bound the gap: scores within 1 % of the model-dtype emulation,
+    and the 20 % top-k blocks chosen from either agree except for blocks whose reference score
+    lies within that 1 % of the k-th largest."""
+    from unifiedkv_amd import compaction, snapkv
+    import torch
+
+    h_kv, n_rep, D, L, sink, obs = 8, 4, 128, 8192, 64, 128
+    rng = np.random.default_rng(77)
+    Kb, Qb = _bits(rng, (h_kv, L, D), dtype), _bits(rng, (h_kv * n_rep, obs, D), dtype)
+    got = snapkv.score_layer_blocks(_dev(Kb, dtype), _dev(Qb, dtype), sink_len=sink, obs_len=obs, n_rep=n_rep)
+    emu = so.score_layer_blocks_model_dtype(_f(Kb, dtype), _f(Qb, dtype), sink_len=sink, obs_len=obs, n_rep=n_rep,
+                                            dtype=dtype)
+    g = got.cpu().numpy().astype(np.float64)
+    assert np.max(np.abs(g - emu) / emu) < 1e-2
+    k = int(0.2 * emu.size)
+    mine = set(compaction.select_blocks(got.view(1, -1).float().contiguous(), k).cpu().numpy()[0].tolist())
+    ref = set(np.argsort(-emu, kind="stable")[:k].tolist())
+    kth = np.sort(emu)[::-1][k - 1]
+    for i in mine ^ ref:
+        assert abs(emu[i] - kth) <= 1e-2 * kth, f"block {i}: {emu[i]} vs k-th {kth}"
