@@ -87,6 +87,31 @@ def test_single_key_returns_v0_and_causality():
     assert not np.allclose(out[4], out2[4])
 
 
+def test_oracle_matches_torch_sdpa_with_a_bottom_right_causal_mask():
+    """torch.nn.functional.scaled_dot_product_attention (CPU, fp32) is the dense attention HF
+    falls back to without flash-attn; with an explicit bottom-right causal mask over
+    prefix + chunk it must give the oracle's values."""
+    import torch
+
+    case = make_case(5, [37, 0, 90], [20, 9, 33], Hq=8, Hkv=2, D=32)
+    out = expected(case)
+    k, v = written_pool(case)
+    f = lambda a: oracle.bits_to_f32(a, oracle.DT_BF16)
+    for b in range(3):
+        L = int(case["kv_lens"][b])
+        C = int(case["cu"][b + 1] - case["cu"][b])
+        if C == 0:
+            continue
+        pages = case["block_table"][b][: (L + 15) // 16]
+        K = torch.tensor(f(k)[pages].reshape(-1, 2, 32)[:L]).transpose(0, 1).repeat_interleave(4, dim=0)
+        V = torch.tensor(f(v)[pages].reshape(-1, 2, 32)[:L]).transpose(0, 1).repeat_interleave(4, dim=0)
+        Q = torch.tensor(f(case["q"])[case["cu"][b]:case["cu"][b + 1]]).transpose(0, 1)
+        mask = torch.arange(L)[None, :] <= (L - C + torch.arange(C))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(Q, K, V, attn_mask=mask, scale=case["scale"])
+        np.testing.assert_allclose(out[case["cu"][b]:case["cu"][b + 1]], ref.transpose(0, 1).numpy(),
+                                   rtol=1e-5, atol=1e-6)
+
+
 # ---------------------------------------------------------------------- GPU
 def to_dev(case, cuda):
     import torch
