@@ -263,9 +263,11 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
   const bool live = i16 < n_here;
 
   const uint16_t* kbase = a.k + (int64_t)(4 * kg) * a.k_st + (int64_t)g * a.k_sh + DPL * i16;
-  // Wave-private LDS rows of the page's K (token-major, padded pitch): rows are
-  // loaded 4 tokens x full width per instruction and read back in MFMA layout.
-  constexpr int KP = D + 8;
+  // Wave-private LDS rows of the page's K (token-major): rows are loaded 4 tokens
+  // x full width per instruction and read back in MFMA layout. The pitch of D + 16
+  // elements (288 B at D = 128) keeps SQ_LDS_BANK_CONFLICT at 0 for the 16-row
+  // reads (D + 8 conflicted on a quarter of the LDS cycles, at the same speed).
+  constexpr int KP = D + 16;
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[UKV_PAGE16_WAVES][16 * KP];
   uint16_t* ks = k_lds[wv];
   const uint16_t* vbase = a.v + (int64_t)(4 * kg) * a.v_st + (int64_t)g * a.v_sh + DPL * i16;
