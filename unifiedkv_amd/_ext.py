@@ -8,6 +8,7 @@ report themselves unavailable, the way the reference reports a missing Triton
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from pathlib import Path
 from typing import Optional
@@ -182,6 +183,12 @@ def status_string(code: int) -> str:
 def i64_array(values) -> ctypes.Array:
     vals = [int(v) for v in values]
     return (ctypes.c_int64 * len(vals))(*vals)
+
+
+@functools.lru_cache(maxsize=512)
+def i64_tuple(values: tuple) -> ctypes.Array:
+    """i64_array of a tuple of ints, built once per distinct tuple (the C side only reads it)."""
+    return i64_array(values)
 
 
 def ptr_array(values) -> ctypes.Array:
