@@ -1,0 +1,109 @@
+"""Host-side argument checks that must fire before any kernel launch (no GPU needed).
+
+Tensors on the ``meta`` device carry shapes, dtypes and strides but no memory, so each
+rejected case below proves that the wrapper raised before it could hand a pointer to
+libukv.so; the accepted shapes then stop at the "must be on a GPU" check.
+"""
+import pytest
+import torch
+
+from unifiedkv_amd import page_ops, snapkv
+from unifiedkv_amd.decode_step import DecodeBatch
+from unifiedkv_amd.pool import PagedKVPool
+from unifiedkv_amd.prefill import PrefillPages
+
+META = torch.device("meta")
+
+
+def _pool_layer(N=8, bs=16, H=2, D=64, dtype=torch.float16, dev=META):
+    return torch.empty((N, bs, H, D), dtype=dtype, device=dev)
+
+
+def _append_args(B=3, H=2, D=64, **over):
+    args = dict(k_layer=_pool_layer(H=H, D=D), v_layer=_pool_layer(H=H, D=D),
+                block_table=torch.empty((B, 4), dtype=torch.int32, device=META),
+                old_lens=torch.empty((B,), dtype=torch.int32, device=META),
+                k_new=torch.empty((B, H, D), dtype=torch.float16, device=META),
+                v_new=torch.empty((B, H, D), dtype=torch.float16, device=META))
+    args.update(over)
+    return args
+
+
+def test_kv_append_accepts_good_shapes_up_to_the_device_check():
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.kv_append(**_append_args())
+    four_d = _append_args(k_new=torch.empty((3, 1, 2, 64), dtype=torch.float16, device=META),
+                          v_new=torch.empty((3, 1, 2, 64), dtype=torch.float16, device=META))
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.kv_append(**four_d)
+
+
+@pytest.mark.parametrize("bad, match", [
+    (dict(old_lens=torch.empty((2,), dtype=torch.int32, device=META)), "old_lens has 2 entries"),
+    (dict(k_new=torch.empty((2, 2, 64), dtype=torch.float16, device=META)), "k_new / v_new must be"),
+    (dict(v_new=torch.empty((3, 4, 64), dtype=torch.float16, device=META)), "k_new / v_new must be"),
+    (dict(k_new=torch.empty((3, 2, 32), dtype=torch.float16, device=META)), "k_new / v_new must be"),
+    (dict(k_new=torch.empty((3, 2, 2, 64), dtype=torch.float16, device=META),
+          v_new=torch.empty((3, 2, 2, 64), dtype=torch.float16, device=META)), r"\[batch, 1, H, D\]"),
+    (dict(k_new=torch.empty((3, 2, 64), dtype=torch.bfloat16, device=META),
+          v_new=torch.empty((3, 2, 64), dtype=torch.bfloat16, device=META)), "pool's dtype"),
+    (dict(old_lens=torch.zeros((3,), dtype=torch.int32)), "old_lens is on cpu"),
+    (dict(block_table=torch.zeros((3, 4), dtype=torch.int32)), "block_table is on cpu"),
+    (dict(k_new=torch.zeros((3, 2, 64), dtype=torch.float16)), "k_new is on cpu"),
+    (dict(v_layer=_pool_layer(N=9)), "equal"),
+    (dict(block_table=torch.empty((3,), dtype=torch.int32, device=META)), r"\[batch, max_blocks\]"),
+])
+def test_kv_append_rejects_before_launch(bad, match):
+    with pytest.raises(RuntimeError, match=match):
+        page_ops.kv_append(**_append_args(**bad))
+
+
+def test_kv_append_rejects_cpu_tensors():
+    cpu = dict(k_layer=_pool_layer(dev="cpu"), v_layer=_pool_layer(dev="cpu"),
+               block_table=torch.zeros((3, 4), dtype=torch.int32), old_lens=torch.zeros((3,), dtype=torch.int32),
+               k_new=torch.zeros((3, 2, 64), dtype=torch.float16), v_new=torch.zeros((3, 2, 64), dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.kv_append(**cpu)
+
+
+def _score_args(seqs=2, layers=2, Hq=8, Hkv=2, obs=16, D=64, table_rows=2, table_dev=META, dev=META):
+    q = torch.empty((seqs, layers, Hq, obs, D), dtype=torch.float16, device=dev)
+    k = torch.empty((layers, 64, 16, Hkv, D), dtype=torch.float16, device=dev)
+    bt = torch.empty((table_rows, 40), dtype=torch.int32, device=table_dev)
+    return q, k, bt
+
+
+def test_score_blocks_rejects_short_or_foreign_tables():
+    q, k, bt = _score_args(table_rows=1)
+    with pytest.raises(RuntimeError, match="bad_score_shape"):
+        snapkv.score_blocks(q, k, bt, seq_len=512, sink_len=16, obs_len=16, n_rep=4)
+    q, k, bt = _score_args(table_dev="cpu")
+    with pytest.raises(RuntimeError, match="bad_score_device"):
+        snapkv.score_blocks(q, k, bt, seq_len=512, sink_len=16, obs_len=16, n_rep=4)
+    q, k, bt = _score_args()
+    with pytest.raises(RuntimeError, match="bad_score_device"):  # meta is not a GPU
+        snapkv.score_blocks(q, k, bt, seq_len=512, sink_len=16, obs_len=16, n_rep=4)
+
+
+class _FakePool:
+    """The attributes DecodeBatch / PrefillPages read before they touch the device."""
+
+    def __init__(self, N=64, B=16, layers=2):
+        self.N_total, self.B, self.num_layers = N, B, layers
+
+
+def test_decode_batch_rejects_lists_shorter_than_their_lengths():
+    pool = _FakePool()
+    with pytest.raises(ValueError, match="length 33 needs 3 pages"):
+        DecodeBatch(pool, [[1, 2], [3, 4, 5]], [33, 33])
+    with pytest.raises(ValueError, match="length 17 needs 2 pages"):
+        DecodeBatch(pool, [[1]], [17])
+
+
+def test_prefill_write_rejects_out_of_range_layers():
+    pp = PrefillPages.__new__(PrefillPages)
+    pp.pool = _FakePool(layers=2)
+    pp._chunk = dict(total=4)
+    for bad in (-1, 2, 7):
+        with pytest.raises(IndexError, match="outside the pool"):
+            pp.write(bad, None, None)

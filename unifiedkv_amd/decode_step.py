@@ -103,6 +103,10 @@ class DecodeBatch:
                 raise ValueError(f"page id outside the pool for seq={sid}")
             if L < 0:
                 raise ValueError(f"negative length for seq={sid}")
+            if -(-L // pool.B) > len(ids):
+                # The device table is zero padded: a length past its list would attend page 0
+                # (another sequence's page) and the fused append would write into it.
+                raise ValueError(f"seq={sid}: length {L} needs {-(-L // pool.B)} pages, its list holds {len(ids)}")
         self.on_pool_full = on_pool_full
         pool.ensure_allocated()
         self.device = pool.device
@@ -149,6 +153,12 @@ class DecodeBatch:
         """Reserve the step's pages and launch the prologue; returns (block_table, attn_lens)."""
         if self._open:
             raise RuntimeError("decode_step_already_open")
+        B = self.pool.B
+        for sid, ids, L in zip(self.seq_ids, self._lists, self._lens):
+            # page_lists hands out the lists themselves: re-check that each still covers its
+            # length (the planner then adds the page a length L % B == 0 needs for its token).
+            if -(-L // B) > len(ids):
+                raise RuntimeError(f"page16_native_blocked:direct_decode_slot_missing seq={sid}")
         try:
             triples = plan_decode_pages(self.pool.allocate_blocks, self._lists, self._lens, self.pool.B,
                                         self.seq_ids, self.on_pool_full)

@@ -116,15 +116,37 @@ def kv_append(k_layer: torch.Tensor, v_layer: torch.Tensor, block_table: torch.T
     for t, w in ((k_layer, "k_layer"), (v_layer, "v_layer"), (k_new, "k_new"), (v_new, "v_new")):
         _check_rows(t, w)
     dev = k_layer.device
+    # Everything the kernel dereferences is checked here, before any launch: a short
+    # length vector or a mis-shaped row tensor would otherwise be read out of bounds.
+    for t, w in ((v_layer, "v_layer"), (k_new, "k_new"), (v_new, "v_new"), (block_table, "block_table"),
+                 (old_lens, "old_lens")):
+        if t.device != dev:
+            raise RuntimeError(f"kv_append: {w} is on {t.device}, the pool layer on {dev}")
+    if k_layer.dim() != 4 or tuple(v_layer.shape) != tuple(k_layer.shape) or v_layer.dtype != k_layer.dtype:
+        raise RuntimeError("kv_append: k_layer / v_layer must be equal [N, bs, H, D] tensors")
+    if block_table.dim() != 2:
+        raise RuntimeError("kv_append: block_table must be [batch, max_blocks]")
     if k_new.dim() == 4:
+        if int(k_new.shape[1]) != 1 or int(v_new.shape[1]) != 1:
+            raise RuntimeError("kv_append: k_new / v_new must be [batch, H, D] or [batch, 1, H, D]")
         k_new, v_new = k_new[:, 0], v_new[:, 0]
+    B = int(block_table.shape[0])
+    want = (B, int(k_layer.shape[2]), int(k_layer.shape[3]))
+    if tuple(k_new.shape) != want or tuple(v_new.shape) != want:
+        raise RuntimeError(f"kv_append: k_new / v_new must be {list(want)}, got {list(k_new.shape)} / "
+                           f"{list(v_new.shape)}")
+    if k_new.dtype != k_layer.dtype or v_new.dtype != k_layer.dtype:
+        raise RuntimeError("kv_append: new rows must have the pool's dtype")
+    if int(old_lens.numel()) != B:
+        raise RuntimeError(f"kv_append: old_lens has {int(old_lens.numel())} entries for a batch of {B}")
+    if dev.type != "cuda":
+        raise RuntimeError(f"kv_append: tensors must be on a GPU, got {dev}")
     if k_new.stride() != v_new.stride():
         v_new = v_new.contiguous()
         k_new = k_new.contiguous()
     bt = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     bt = bt.contiguous()
     lens = old_lens.to(torch.int32).contiguous()
-    B = int(bt.shape[0])
     new_lens = torch.empty_like(lens) if return_new_lens else None
     code = _ext.load().ukv_kv_append(
         k_layer.data_ptr(), v_layer.data_ptr(), _ext.i64_array(k_layer.stride()[:3]),

@@ -192,9 +192,12 @@ class PrefillPages:
     def write(self, layer_id: int, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """The layer's chunk K/V, packed [total_q, H_kv, D] in batch order, into their pages."""
         c = self._open()
+        pool = self.pool
+        layer_id = int(layer_id)
+        if not 0 <= layer_id < pool.num_layers:  # the fast path below computes the layer's address itself
+            raise IndexError(f"layer {layer_id} is outside the pool's {pool.num_layers} layers")
         if c["total"] == 0:
             return
-        pool = self.pool
         if (k_new.dtype != pool.dtype or v_new.dtype != pool.dtype or k_new.device != self.dev
                 or tuple(k_new.shape) != (c["total"], pool.num_kv_heads, pool.head_dim)
                 or k_new.stride() != v_new.stride() or k_new.stride(-1) != 1):

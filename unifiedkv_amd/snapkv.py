@@ -89,6 +89,13 @@ def score_blocks(q_obs: torch.Tensor, k_pool: torch.Tensor, block_table: torch.T
         return out
     if q_obs.dtype not in _DTYPES or k_pool.dtype != q_obs.dtype:
         raise RuntimeError("selected_writeback_bad_score_shape")
+    # The kernel reads table rows 0 .. seqs-1 on q_obs's device: check both before any launch.
+    if k_pool.device != q_obs.device or block_table.device != q_obs.device:
+        raise RuntimeError("selected_writeback_bad_score_device")
+    if block_table.dim() != 2 or int(block_table.shape[0]) < seqs:
+        raise RuntimeError("selected_writeback_bad_score_shape")
+    if q_obs.device.type != "cuda":
+        raise RuntimeError("selected_writeback_bad_score_device")
     if q_obs.stride(4) != 1 or q_obs.stride(0) != layers * q_obs.stride(1):
         q_obs = q_obs.contiguous()
     if block_table.dtype != torch.int32:
