@@ -5,7 +5,8 @@
  * enqueues its kernels on the given HIP stream and returns without a host
  * synchronisation. Return value: UKV_OK (0) or a negative ukv_status.
  * No entry point allocates device memory: scratch space is passed in as a
- * workspace whose size the matching *_workspace_bytes() call reports.
+ * workspace whose size the matching *_workspace_bytes() call reports, except for
+ * ukv_page16_decode_noalloc, whose scratch is a fixed device array of the library.
  *
  * Reference interfaces replaced (paths relative to the BP-KV repository):
  *   ukv_page16_decode      core/page16_native.py:83-150 page16_decode_attention
@@ -107,6 +108,26 @@ int ukv_page16_decode(const void* q, const void* k_cache, const void* v_cache,
                       int max_blocks, int num_pages, const int64_t* q_strides,
                       const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
                       int dtype, void* workspace, size_t workspace_bytes, ukv_stream_t stream);
+
+/*
+ * ukv_page16_decode without a workspace argument: the split-K scratch is a device array of
+ * the library (UKV_PAGE16_SCRATCH_BYTES per GPU, held by each GPU the library runs on until
+ * the process ends), so the call allocates nothing - no hipMalloc, hipFree or allocating
+ * library routine. Same arguments (less the workspace), semantics and result as
+ * ukv_page16_decode; UKV_ERR_WORKSPACE (nothing launched) when the shape needs more than
+ * UKV_PAGE16_SCRATCH_BYTES (ukv_page16_workspace_bytes), UKV_ERR_NO_DEVICE when the array's
+ * address cannot be read on the current device. Every call on one GPU uses that GPU's one
+ * array: calls that overlap there (two streams, two host threads) race.
+ * No counterpart in the reference: this is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ */
+#define UKV_PAGE16_SCRATCH_BYTES ((size_t)32 << 20)
+int ukv_page16_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* seqlens, void* out,
+                              int batch, int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                              int max_blocks, int num_pages, const int64_t* q_strides,
+                              const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
+                              int dtype, ukv_stream_t stream);
 
 /*
  * Decode with the step's token append fused in: the same result as ukv_kv_append with

@@ -52,6 +52,17 @@ SIGNATURES = {
             _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
         ],
     ),
+    "ukv_page16_decode_noalloc": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p,  # q, k_cache, v_cache
+            _c_void_p, _c_void_p, _c_void_p,  # block_table, seqlens, out
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # batch, Hq, Hkv, D, n_rep
+            _c_int, _c_int,  # max_blocks, num_pages
+            _c_i64p, _c_i64p, _c_i64p,  # q/k/v strides
+            ctypes.c_float, _c_int, _c_void_p,  # softmax_scale, dtype, stream
+        ],
+    ),
     "ukv_kv_scatter_tokens": (
         _c_int,
         [_c_void_p, _c_i64p, _c_void_p, _c_i64p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

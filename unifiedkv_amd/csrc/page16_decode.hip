@@ -858,6 +858,51 @@ extern "C" int ukv_page16_decode(const void* q, const void* k_cache, const void*
                      workspace_bytes, stream_handle, nullptr);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split-K workspace lives in a file-scope device
+// array instead of a caller buffer. Each GPU holds its own copy of the array
+// (UKV_PAGE16_SCRATCH_BYTES, for the life of the process) at its own address;
+// host code reaches it only through the address hipGetSymbolAddress reports for
+// the current device, read once per device on the first call there. Calls that
+// overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[UKV_PAGE16_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device (nullptr on failure).
+void* scratch_address() {
+  static std::atomic<void*> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = cached[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  // Racing first calls on one device store the same address.
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+  cached[dev].store(p, std::memory_order_release);
+  return p;
+}
+
+}  // namespace
+
+extern "C" int ukv_page16_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                         const int32_t* block_table, const int32_t* seqlens, void* out, int batch,
+                                         int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks,
+                                         int num_pages, const int64_t* q_strides, const int64_t* k_strides,
+                                         const int64_t* v_strides, float softmax_scale, int dtype,
+                                         ukv_stream_t stream_handle) {
+  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0) return UKV_ERR_EMPTY;
+  if (ukv_page16_workspace_bytes(batch, num_q_heads, head_dim, max_blocks) > UKV_PAGE16_SCRATCH_BYTES)
+    return UKV_ERR_WORKSPACE;
+  void* ws = scratch_address();
+  if (!ws) return UKV_ERR_NO_DEVICE;
+  return decode_impl(q, k_cache, v_cache, block_table, seqlens, out, batch, num_q_heads, num_kv_heads, head_dim,
+                     n_rep, max_blocks, num_pages, q_strides, k_strides, v_strides, softmax_scale, dtype, ws,
+                     UKV_PAGE16_SCRATCH_BYTES, stream_handle, nullptr);
+}
+
 extern "C" int ukv_page16_decode_append(const void* q, void* k_cache, void* v_cache, const int32_t* block_table,
                                         const int32_t* seqlens, const void* k_new, const void* v_new,
                                         const int64_t* new_strides, void* out, int batch, int num_q_heads,
