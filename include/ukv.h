@@ -19,6 +19,10 @@
  *   ukv_kv_append          core/scheduler.py:401-408 decode-token scatter into the pool
  *   ukv_copy_2d            core/offload.py:577-597, 662-680 per-page pinned copies (one strided copy per chunk)
  *   ukv_page16_decode_append  core/scheduler.py:401-418 that scatter fused with the decode call
+ *   ukv_retain_writeback_dense  core/scheduler.py:702-733, 735-799 selected writeback of dense raw KV
+ *                          (block-indexed and token-granular), all layers of a sequence in one launch
+ *   ukv_retain_compact_pages    the same map over pool-resident pages; core/offload.py:1236-1258
+ *                          prune_sequence_window's pool->pool copy
  *   ukv_decode_prologue    core/offload.py:780-866 reserve_decode_slot (table side),
  *                          core/scheduler.py:1092-1160 per-layer table / cache_seqlens build,
  *                          core/scheduler.py:1247-1265 commit (seq_len += 1)
@@ -186,6 +190,54 @@ int ukv_page_copy(const void* const* src_pools, void* const* dst_pools, int npoo
                   const int64_t* dst_strides, const int32_t* src_ids, int64_t src_ids_layer_stride,
                   const int32_t* dst_ids, int64_t dst_ids_layer_stride, int n, int layers, int page_elems,
                   int src_pages, int dst_pages, ukv_stream_t stream);
+
+/*
+ * Retain-set writeback: one launch writes the retained tokens of every layer of one sequence into
+ * its destination pages (dst_ids, shared by every layer; [layers, num_pages, 16, num_heads,
+ * head_dim] K/V pools with element strides pool_strides = {layer, page, slot, head}). Destination
+ * position p < dst_len of layer l takes source token
+ *   p                                          if p < sink_len;
+ *   sink_len + 16*sel[l*sel_layer_stride + j] + r,  j = (p - sink_len)/16, r = (p - sink_len)%16,
+ *                                              if p < sink_len + 16*k; when that token is not below
+ *                                              mid_end = max(sink_len, src_len - obs_len) (or the
+ *                                              entry is negative) the row is zero if pad_blocks,
+ *                                              else not written;
+ *   obs_start + (p - sink_len - 16*k)          otherwise, obs_start = max(0, src_len - obs_len);
+ * dst_len = sink_len + 16*k + (src_len - obs_start), and position p goes to page dst_ids[p/16],
+ * slot p%16 (slots past dst_len are not written). This is the SnapKV compaction layout - the sink,
+ * each selected middle block zero-padded to 16 tokens, the observation window - at any alignment.
+ * Requires sink_len <= src_len, dst_len <= 16*n_dst_ids, head_dim % 8 == 0 and 16-byte aligned
+ * rows, else UKV_ERR_INVALID_ARGUMENT; destination ids outside [0, num_pages) skip their page.
+ *
+ * ukv_retain_writeback_dense: sources are the scheduler's dense raw K/V of each layer,
+ * k_layers[l] / v_layers[l] (HOST arrays of `layers` device pointers) [num_heads, src_len,
+ * head_dim] with element strides dense_strides = {head, token}. Replaces the per-layer selected
+ * writeback of core/scheduler.py:735-799 (_write_selected_layer_to_pool: the block-aligned fast
+ * path's index_select -> permute().contiguous() -> index_put of _write_block_indexed_layer_to_pool
+ * :702-733, with sink_len = obs_len = 0 and sel = the source blocks, and the token-granular
+ * _write_piece_to_blocks :666-690 / _pad_piece_to_block :692-700 path) for all layers of a
+ * sequence at once (core/scheduler.py:826-848).
+ *
+ * ukv_retain_compact_pages: sources are pool-resident pages, token t of layer l at page
+ * src_ids[t/16], slot t%16 of k_src_pool / v_src_pool (strides src_strides = {layer, page, slot,
+ * head}; ids outside [0, src_num_pages) skip the token); src_len <= 16*n_src_ids. Source and
+ * destination pages must not overlap. With sink_len = obs_len = 0, pad_blocks = 0 and sel = the
+ * kept blocks in ascending order, shared by all layers (sel_layer_stride 0), this is the
+ * pool->pool copy of core/offload.py:1236-1258 (prune_sequence_window: each kept block's tokens,
+ * a partial last block included, concatenated into new pages); with the SnapKV map it is the
+ * selected writeback of a sequence whose KV is already in pages.
+ */
+int ukv_retain_writeback_dense(const void* const* k_layers, const void* const* v_layers, const int64_t* dense_strides,
+                               int src_len, int sink_len, int obs_len, const int32_t* sel, int64_t sel_layer_stride,
+                               int k, int pad_blocks, void* k_pool, void* v_pool, const int64_t* pool_strides,
+                               const int32_t* dst_ids, int n_dst_ids, int num_pages, int layers, int num_heads,
+                               int head_dim, ukv_stream_t stream);
+int ukv_retain_compact_pages(const void* k_src_pool, const void* v_src_pool, const int64_t* src_strides,
+                             const int32_t* src_ids, int n_src_ids, int src_num_pages, int src_len, int sink_len,
+                             int obs_len, const int32_t* sel, int64_t sel_layer_stride, int k, int pad_blocks,
+                             void* k_pool, void* v_pool, const int64_t* pool_strides, const int32_t* dst_ids,
+                             int n_dst_ids, int num_pages, int layers, int num_heads, int head_dim,
+                             ukv_stream_t stream);
 
 /*
  * Decode-step append: for each sequence b with len = old_lens[b], write k_new[b] / v_new[b]

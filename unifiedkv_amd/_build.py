@@ -22,6 +22,7 @@ SOURCES = [
     "ukv_runtime.hip",
     "page16_decode.hip",
     "page_ops.hip",
+    "retain_copy.hip",
     "select.hip",
     "paged_prefill.hip",
     "snapkv_score.hip",

@@ -82,6 +82,29 @@ SIGNATURES = {
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # n, layers, page_elems, src/dst pages, stream
         ],
     ),
+    "ukv_retain_writeback_dense": (
+        _c_int,
+        [
+            ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p), _c_i64p,  # k/v layer bases (host), strides
+            _c_int, _c_int, _c_int,  # src_len, sink_len, obs_len
+            _c_void_p, ctypes.c_int64, _c_int, _c_int,  # sel, sel layer stride, k, pad_blocks
+            _c_void_p, _c_void_p, _c_i64p,  # k/v pools, pool strides
+            _c_void_p, _c_int, _c_int,  # dst ids, n_dst_ids, num_pages
+            _c_int, _c_int, _c_int, _c_void_p,  # layers, heads, head_dim, stream
+        ],
+    ),
+    "ukv_retain_compact_pages": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_i64p,  # k/v source pools, strides
+            _c_void_p, _c_int, _c_int, _c_int,  # src ids, n_src_ids, src_num_pages, src_len
+            _c_int, _c_int,  # sink_len, obs_len
+            _c_void_p, ctypes.c_int64, _c_int, _c_int,  # sel, sel layer stride, k, pad_blocks
+            _c_void_p, _c_void_p, _c_i64p,  # k/v pools, pool strides
+            _c_void_p, _c_int, _c_int,  # dst ids, n_dst_ids, num_pages
+            _c_int, _c_int, _c_int, _c_void_p,  # layers, heads, head_dim, stream
+        ],
+    ),
     "ukv_kv_append": (
         _c_int,
         [
