@@ -1,0 +1,193 @@
+"""BASELINE config 5 at its full size on the GPU: 32 layers x 8 sequences x 2048 fragmented pages.
+
+(a) compaction: select_blocks -> retained_pages -> compact. The page lists equal the oracle's
+    FIFO lists replayed on a FifoAllocator, the device table equals build_block_table of them,
+    and for every layer pool[l, dst] equals pool[l, src] with the sources of the oracle's
+    selection (core/scheduler.py:805-878). The token-granular kernel (compact_selected) then
+    produces the same bytes in other pages, and the free list matches the oracle's throughout.
+(b) offload / prefetch: the 27.3 GB of evicted pages (1629 per layer and sequence) through
+    pinned host memory onto newly allocated ids, bit-exact per layer (core/offload.py:547-691).
+(c) decode at B=8, L=6704 on the compacted tables: two sampled sequences of two layers against
+    the fp64 oracle (|gpu - oracle| <= 2e-3 + 1e-2 |oracle|), and bit-identical output after a
+    random relabelling of every physical page.
+"""
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import compaction_oracle as co
+from oracle import oracle, pool_oracle
+from unifiedkv_amd import compaction, page16_native
+from unifiedkv_amd.pool import PagedKVPool
+from unifiedkv_amd.staging import PageStager
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, SEQS, CTX, HKV, HQ, D, SINK, OBS, RATIO = 32, 8, 32768, 8, 32, 128, 64, 128, 0.20
+PER = CTX // 16  # 2048 pages per sequence
+SEED = 5
+
+
+def log(msg):
+    print(f"[config5] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def c5(cuda):
+    k_blocks, eff, mode = compaction.selection_budget_blocks(CTX, sink_len=SINK, obs_len=OBS, retain_ratio=RATIO)
+    assert (k_blocks, eff, mode) == (407, 6704, "ratio")
+    keep = eff // 16
+    evict = PER - keep
+    # sources + two compactions + the prefetch targets
+    N = SEQS * PER + 2 * SEQS * keep + SEQS * evict
+    log(f"pool {N} pages x {LAYERS} layers ({2 * N * LAYERS * 16 * HKV * D * 2 / 1e9:.1f} GB)")
+    pool = PagedKVPool(16, LAYERS, HKV, D, torch.bfloat16, num_blocks=N, device=cuda)
+    alloc = pool_oracle.FifoAllocator(N)
+    rng = np.random.default_rng(SEED)
+    # a shuffled free list, so that every sequence's pages are fragmented
+    order = [int(x) for x in rng.permutation(N)]
+    assert pool.allocate_blocks(N) == alloc.allocate_blocks(N)
+    pool.free_blocks_by_ids(order)
+    alloc.free_blocks_by_ids(order)
+    lists = [pool.allocate_blocks(PER) for _ in range(SEQS)]
+    assert lists == [alloc.allocate_blocks(PER) for _ in range(SEQS)]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(SEED)
+    used = torch.tensor(sorted(p for ids in lists for p in ids), dtype=torch.long, device=cuda)
+    for layer in range(LAYERS):
+        for lo in range(0, used.numel(), 2048):
+            idx = used[lo:lo + 2048]
+            for cache in (pool.k_cache, pool.v_cache):
+                cache[layer, idx] = torch.randn((idx.numel(), 16, HKV, D), generator=g, device=cuda).to(torch.bfloat16)
+    scores = rng.random((SEQS * LAYERS, PER - (SINK + OBS) // 16), dtype=np.float32)
+    torch.cuda.synchronize()
+    log("pool filled")
+    state = dict(pool=pool, alloc=alloc, lists=lists, scores=scores, k=k_blocks, eff=eff, keep=keep, evict=evict)
+    yield state
+    state.clear()
+    del pool
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def _src_ids(lists, ret):
+    """Physical source ids per sequence: [layers, keep] from the oracle's retained logical pages."""
+    return [np.asarray(pages)[r] for pages, r in zip(lists, ret)]
+
+
+def test_a_compaction_full_size(c5, cuda):
+    pool, alloc, lists = c5["pool"], c5["alloc"], c5["lists"]
+    scores = torch.from_numpy(c5["scores"]).to(cuda)
+    sel = compaction.select_blocks(scores, c5["k"])
+    retained = [compaction.retained_pages(CTX, sel[b * LAYERS:(b + 1) * LAYERS], sink_len=SINK, obs_len=OBS)
+                for b in range(SEQS)]
+    res = compaction.compact(pool, lists, retained, [c5["eff"]] * SEQS)
+    log("compact done")
+    sel_np = co.select_topk(c5["scores"], c5["k"])
+    ret_np = [co.retained_pages(CTX, sel_np[b * LAYERS:(b + 1) * LAYERS], 16, SINK, OBS) for b in range(SEQS)]
+    for a, b in zip(retained, ret_np):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+    # the oracle's compaction on a stand-in pool of one byte per page: same FIFO lists
+    tiny = np.zeros((LAYERS, pool.N_total, 1), dtype=np.int8)
+    exp_lists = co.compact(tiny, tiny.copy(), alloc, lists, ret_np)
+    assert res.page_lists == exp_lists
+    assert pool.free_blocks == alloc.free_blocks
+    np.testing.assert_array_equal(res.block_table.cpu().numpy(), pool_oracle.build_block_table(exp_lists))
+    srcs = _src_ids(lists, ret_np)
+    dst = torch.tensor([p for ids in exp_lists for p in ids], dtype=torch.long, device=cuda)
+    for layer in range(LAYERS):
+        src = torch.from_numpy(np.concatenate([s[layer] for s in srcs])).to(cuda).long()
+        assert torch.equal(pool.k_cache[layer, dst], pool.k_cache[layer, src]), f"K layer {layer}"
+        assert torch.equal(pool.v_cache[layer, dst], pool.v_cache[layer, src]), f"V layer {layer}"
+    log("compact bit-exact on every layer")
+    # the token-granular kernel on the same selection: the same bytes in a second set of pages
+    mids = [sel[b * LAYERS:(b + 1) * LAYERS] for b in range(SEQS)]
+    res2 = compaction.compact_selected(pool, lists, [CTX] * SEQS, mids, sink_len=SINK, obs_len=OBS)
+    exp2 = [alloc.allocate_blocks(c5["keep"]) for _ in range(SEQS)]
+    assert res2.page_lists == exp2 and res2.seq_lens == [c5["eff"]] * SEQS
+    assert pool.free_blocks == alloc.free_blocks
+    dst2 = torch.tensor([p for ids in exp2 for p in ids], dtype=torch.long, device=cuda)
+    for layer in range(LAYERS):
+        assert torch.equal(pool.k_cache[layer, dst2], pool.k_cache[layer, dst]), f"K layer {layer}"
+        assert torch.equal(pool.v_cache[layer, dst2], pool.v_cache[layer, dst]), f"V layer {layer}"
+    log("compact_selected equals compact on every layer")
+    c5.update(res=res, ret_np=ret_np)
+
+
+def test_b_offload_round_trip_full_size(c5, cuda):
+    if "ret_np" not in c5:
+        pytest.skip("needs the compaction of test_a_compaction_full_size")
+    pool, alloc, lists = c5["pool"], c5["alloc"], c5["lists"]
+    ret_np = c5["ret_np"]
+    evicted = []
+    for b in range(SEQS):
+        table = np.asarray(lists[b])
+        evicted.append(np.stack([table[np.setdiff1d(np.arange(PER), ret_np[b][l])] for l in range(LAYERS)]))
+    ev = np.concatenate(evicted, axis=1).astype(np.int32)  # [layers, 8 * 1629]
+    n = ev.shape[1]
+    assert n == SEQS * c5["evict"] == 13032
+    new = pool.allocate_blocks(n)
+    assert new == alloc.allocate_blocks(n)
+    stager = PageStager(pool, chunk_pages=512)
+    log(f"offload {2 * LAYERS * n * 16 * HKV * D * 2 / 1e9:.2f} GB")
+    host = stager.offload(torch.from_numpy(ev))
+    event = stager.prefetch(host, torch.tensor(new, dtype=torch.int32))
+    stager.wait(event)
+    torch.cuda.synchronize()
+    log("round trip done")
+    ev_d = torch.from_numpy(ev).to(cuda).long()
+    new_d = torch.tensor(new, dtype=torch.long, device=cuda)
+    for layer in range(LAYERS):
+        assert torch.equal(pool.k_cache[layer, new_d], pool.k_cache[layer, ev_d[layer]]), f"K layer {layer}"
+        assert torch.equal(pool.v_cache[layer, new_d], pool.v_cache[layer, ev_d[layer]]), f"V layer {layer}"
+    del host, stager
+    gc.collect()
+    if hasattr(torch._C, "_host_emptyCache"):  # give the 27 GB of pinned host memory back
+        torch._C._host_emptyCache()
+    log("round trip bit-exact on every layer")
+
+
+def test_c_decode_on_compacted_tables(c5, cuda):
+    if "res" not in c5:
+        pytest.skip("needs the compaction of test_a_compaction_full_size")
+    pool, res = c5["pool"], c5["res"]
+    eff = c5["eff"]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(SEED + 7)
+    q = torch.randn((SEQS, HQ, D), generator=g, device=cuda).to(torch.bfloat16)
+    lens = torch.full((SEQS,), eff, dtype=torch.int32, device=cuda)
+    table = res.block_table
+    assert tuple(table.shape) == (SEQS, eff // 16)
+    scale = D ** -0.5
+    rng = np.random.default_rng(SEED + 11)
+    for layer in (0, LAYERS - 1):
+        out = page16_native.page16_decode_attention(q, pool.k_cache[layer], pool.v_cache[layer], table, lens,
+                                                    softmax_scale=scale, n_rep=HQ // HKV)
+        got = out.float().cpu().numpy()
+        for b in sorted(rng.choice(SEQS, 2, replace=False)):
+            ids = torch.tensor(res.page_lists[b], dtype=torch.long, device=cuda)
+            kb = pool.k_cache[layer, ids].float().cpu().numpy()
+            vb = pool.v_cache[layer, ids].float().cpu().numpy()
+            exp = oracle.page16_decode_dense(q[b:b + 1].float().cpu().numpy(), kb, vb,
+                                             np.arange(eff // 16, dtype=np.int32)[None], np.array([eff], np.int32),
+                                             softmax_scale=scale, n_rep=HQ // HKV)
+            ok, err, excess = oracle.allclose_report(got[b:b + 1], exp, 2e-3, 1e-2)
+            assert ok, f"layer {layer} seq {b}: max abs err {err:.3e}"
+            log(f"layer {layer} seq {b}: max abs err {err:.2e}")
+        # relabel every page of the batch: a new one-layer pool holding the same pages elsewhere
+        flat = torch.tensor([p for ids in res.page_lists for p in ids], dtype=torch.long, device=cuda)
+        M = flat.numel() + 97
+        dest = torch.from_numpy(rng.permutation(M)[:flat.numel()]).to(cuda)
+        k2 = torch.zeros((M, 16, HKV, D), dtype=torch.bfloat16, device=cuda)
+        v2 = torch.zeros_like(k2)
+        k2[dest] = pool.k_cache[layer, flat]
+        v2[dest] = pool.v_cache[layer, flat]
+        remap = torch.full((pool.N_total,), -1, dtype=torch.long, device=cuda)
+        remap[flat] = dest
+        table2 = remap[table.long()].to(torch.int32)
+        out2 = page16_native.page16_decode_attention(q, k2, v2, table2, lens, softmax_scale=scale, n_rep=HQ // HKV)
+        assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), f"layer {layer}: relabelling changed it"
+        del k2, v2
+    log("decode on compacted tables matches")
