@@ -155,6 +155,46 @@ def test_stale_workspace_with_fewer_pages_than_workgroups(cuda):
         assert_close(got, exp, f"stale workspace filled with {fill:#x}")
 
 
+def test_one_workspace_serves_shapes_back_to_back(cuda):
+    # One workspace serves calls of different shapes back to back (long, ragged, single-page
+    # and empty sequences, several q-head groupings), each reading the partials the previous
+    # call left behind as garbage; each call must match the oracle.
+    from unifiedkv_amd import _ext
+
+    torch = _torch()
+    lib = _ext.load()
+    ws = torch.full((64 << 20,), 0x7F, dtype=torch.uint8, device=cuda)
+    shapes = [(4, 32, 8, 128, [3000, 17, 1, 2048], 200), (9, 16, 2, 64, [0, 700, 5000, 33, 64, 1, 900, 12, 3], 320),
+              (2, 64, 8, 128, [40000, 1], 2500), (5, 8, 8, 256, [600, 0, 1200, 48, 16], 80)]
+    for i, (B, Hq, Hkv, D, lens, mb) in enumerate(shapes):
+        case = custom_case(300 + i, B, Hq, Hkv, D, lens, max_blocks=mb)
+        tc = workloads.to_torch(case)
+        out = torch.empty_like(tc["q"])
+        rc = lib.ukv_page16_decode(
+            tc["q"].data_ptr(), tc["k_cache"].data_ptr(), tc["v_cache"].data_ptr(), tc["block_table"].data_ptr(),
+            tc["seqlens"].data_ptr(), out.data_ptr(), B, Hq, Hkv, D, Hq // Hkv, mb, case["N"],
+            _ext.i64_array(tc["q"].stride()[:2]), _ext.i64_array(tc["k_cache"].stride()[:3]),
+            _ext.i64_array(tc["v_cache"].stride()[:3]), case["scale"], _ext.UKV_DTYPE_BF16, ws.data_ptr(),
+            ws.numel(), torch.cuda.current_stream().cuda_stream)
+        assert rc == _ext.UKV_OK
+        assert_close(to_f32(out), expected_dense(case), f"shape {i}")
+
+
+def test_batch_of_4200_short_sequences(cuda):
+    # 4200 sequences of 0..48 tokens: every workgroup holds many whole and split sequences,
+    # and the combine walks 4200 x 32 (sequence, head) merges. Empty sequences give NaN.
+    torch = _torch()
+    B = 4200
+    rng = np.random.default_rng(77)
+    lens = rng.integers(0, 49, B)
+    case = custom_case(78, B, 32, 8, 128, [int(x) for x in lens], max_blocks=3)
+    out = to_f32(decode_gpu(workloads.to_torch(case)))
+    exp = expected_dense(case)
+    assert np.isnan(out[lens == 0]).all()
+    assert_close(out, exp, "4200-sequence batch")
+    torch.cuda.synchronize()
+
+
 def test_invalid_page_ids_are_masked(cuda):
     case = custom_case(24, 2, 32, 8, 128, [64, 48])
     case["block_table"] = case["block_table"].copy()

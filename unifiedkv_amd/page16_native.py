@@ -96,9 +96,28 @@ def _workspace_bytes(dev_index, batch, num_q_heads, head_dim, max_blocks) -> int
         return max(int(_ext.load().ukv_page16_workspace_bytes(batch, num_q_heads, head_dim, max_blocks)), 256)
 
 
-def _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev) -> torch.Tensor:
-    ws_bytes = _workspace_bytes(dev.index, batch, num_q_heads, head_dim, max_blocks)
-    return torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+# One workspace per (device, stream), reused by every call on that stream (calls on one stream
+# are ordered; the workspace needs no initialisation, include/ukv.h). A workspace outgrown by a
+# larger shape is replaced and the old one kept alive, since a captured graph may still use it.
+# Under graph capture a missing or small workspace is allocated for that call alone (it then
+# belongs to the graph's memory pool), never cached.
+_WORKSPACES = {}
+_RETIRED = []
+
+
+def _workspace(batch, num_q_heads, head_dim, max_blocks, dev, stream) -> torch.Tensor:
+    need = _workspace_bytes(dev.index, batch, num_q_heads, head_dim, max_blocks)
+    key = (dev.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is not None and ws.numel() >= need:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(need, dtype=torch.uint8, device=dev)
+    fresh = torch.empty(need if ws is None else max(need, 2 * ws.numel()), dtype=torch.uint8, device=dev)
+    if ws is not None:
+        _RETIRED.append(ws)
+    _WORKSPACES[key] = fresh
+    return fresh
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -139,8 +158,8 @@ def page16_decode_attention(
     num_pages = min(int(k_cache.shape[0]), int(v_cache.shape[0]))
 
     lib = _ext.load()
-    workspace = _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev)
     stream = _current_stream(dev)
+    workspace = _workspace(batch, num_q_heads, head_dim, max_blocks, dev, stream)
     code = lib.ukv_page16_decode(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         block_table.data_ptr(), cache_seqlens.data_ptr(), out.data_ptr(),
@@ -198,8 +217,8 @@ def page16_decode_append_attention(
     num_pages = min(int(k_cache.shape[0]), int(v_cache.shape[0]))
 
     lib = _ext.load()
-    workspace = _workspace(lib, batch, num_q_heads, head_dim, max_blocks, dev)
     stream = _current_stream(dev)
+    workspace = _workspace(batch, num_q_heads, head_dim, max_blocks, dev, stream)
     code = lib.ukv_page16_decode_append(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         block_table.data_ptr(), cache_seqlens.data_ptr(),
