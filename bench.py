@@ -58,17 +58,38 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# The sources the decode kernels are compiled from: a PMC summary applies to a build only when
+# these hash the same as when it was measured.
+DECODE_SOURCES = ("unifiedkv_amd/csrc/page16_decode.hip", "unifiedkv_amd/csrc/ukv_common.h", "include/ukv.h",
+                  "unifiedkv_amd/_build.py")
+
+
+def decode_sources_sha256() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        h.update(rel.encode() + b"\0" + (ROOT / rel).read_bytes() + b"\0")
+    return h.hexdigest()
+
+
 def pmc_traffic_bytes():
-    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if any."""
+    """(HBM bytes per decode step, note) from the committed rocprofv3 --pmc summary: the bytes only
+    when the summary was measured on decode sources identical to the ones this build uses."""
     if not PMC_SUMMARY.exists():
-        return None
+        return None, "no PMC summary committed"
+    fields = {}
     for line in PMC_SUMMARY.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_step:"):
-            try:
-                return int(float(line.split(":", 1)[1].split()[0]))
-            except ValueError:
-                return None
-    return None
+        if ":" in line and not line.startswith(" "):
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip()
+    measured = fields.get("decode_sources_sha256")
+    if measured != decode_sources_sha256():
+        return None, "the PMC summary was measured on other decode kernel sources"
+    try:
+        return int(float(fields["traffic_bytes_per_step"].split()[0])), f"PMC summary at {fields.get('measured_at', '?')}"
+    except (KeyError, ValueError):
+        return None, "the PMC summary holds no traffic line"
 
 
 def event_time_ms(fn, steps, warmup=0):
@@ -228,6 +249,7 @@ def decode_record(layout, tc, args, workload, metric, *, with_pmc=False, rotate=
         log("[bench] timing the CPU baseline sample")
         cpu = cpu_baseline(tc, layout, args.cpu_seconds)
         cpu["us_per_step_equiv"] = round(step_bytes / (cpu["value"] * 1e9) * 1e6, 1)
+    traffic, traffic_note = pmc_traffic_bytes() if with_pmc else (None, "no PMC summary for this workload")
     return {
         "metric": metric,
         "value": round(gbps, 2),
@@ -253,7 +275,7 @@ def decode_record(layout, tc, args, workload, metric, *, with_pmc=False, rotate=
         "algorithmic_bytes_per_step": step_bytes,
         "roofline": {
             "bound": "hbm", "achieved": round(kern_gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": round(kern_gbps / PEAK_HBM_GBPS, 4), "traffic": pmc_traffic_bytes() if with_pmc else None,
+            "frac": round(kern_gbps / PEAK_HBM_GBPS, 4), "traffic": traffic, "traffic_source": traffic_note,
             "kernel_us": round(kern_ms * 1e3, 2),
             "kernel_us_median": round(sorted(per_ms)[len(per_ms) // 2] * 1e3, 2),
         },
