@@ -24,9 +24,10 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
   --workload offload           config 5b: evicted pages -> pinned host -> new pages
   --workload compacted_decode  config 5c: decode B=8 at L=6704 on the compacted tables,
                                rotating through the 32 layers
-  --workload step              a 32-layer decode step on the config-2 batch: prologue + fused
-                               append/decode per layer, beside the unfused kernels and the
-                               reference's call pattern (step_ragged: the config-3 batch)
+  --workload step              a 32-layer decode step on the config-2 batch: prologue, then per
+                               layer the append kernel and the decode, beside the fused
+                               append/decode and the reference's call pattern (step_ragged:
+                               the config-3 batch)
   --workload offload_seq       config 5b's volume through the per-sequence offload / prefetch entry
                                points over the pinned page arena, beside the reference's per-page pattern
   --workload prefill_pages     config 4's sequences prefilled in 2048-token chunks over 32 layers with
@@ -310,11 +311,12 @@ def run_decode(args, dev):
 # ------------------------------------------------------------------- 32-layer decode step
 def run_step(args, dev):
     """One decode step of a 32-layer model over the config-2 (or config-3) batch: the step's
-    prologue (new pages + attention lengths, once) and per layer the fused append + decode.
-    Beside it, on the same pool and batch: the same kernels unfused (append kernel, then
-    decode), and the reference's call pattern (core/scheduler.py:1092-1160, 401-418: per-row
-    table uploads per layer, torch index_put of the token, attn_lens = old + 1) with this
-    build's decode kernel, so the difference is the prologue's and the fusion's."""
+    prologue (new pages + attention lengths, once) and per layer the append kernel and the
+    decode (DecodeBatch's default). Beside it, on the same pool and batch and interleaved with
+    it: the append fused into the decode kernel (DecodeBatch(fused_append=True)), and the
+    reference's call pattern (core/scheduler.py:1092-1160, 401-418: per-row table uploads per
+    layer, torch index_put of the token, attn_lens = old + 1) with this build's decode kernel,
+    so the difference is the prologue's."""
     import numpy as np
     import torch
 
@@ -348,34 +350,32 @@ def run_step(args, dev):
     log(f"[bench] step: {n_layers} layers, pool {N} pages/layer "
         f"({2 * pool.k_cache.numel() * 2 / 2**30:.1f} GiB)")
 
-    # (a) prologue + fused append/decode
-    fused = DecodeBatch(pool, [list(x) for x in lists0], lens0)
+    # (a) DecodeBatch's default: prologue + per layer append kernel and decode;
+    # (b) the same with the append fused into the decode kernel (opt-in). Timed interleaved.
+    batches = {"append_then_decode": DecodeBatch(pool, [list(x) for x in lists0], lens0),
+               "fused_append": DecodeBatch(pool, [list(x) for x in lists0], lens0, fused_append=True)}
     lens_log = []
 
-    def step_fused():
-        lens_log.append(fused.seq_lens)
-        fused.begin_step()
-        for l in range(n_layers):
-            fused.attention(l, qs[l], kns[l], vns[l], softmax_scale=scale, n_rep=n_rep)
-        fused.end_step()
+    def make_step(batch):
+        def step():
+            lens_log.append(batch.seq_lens)
+            batch.begin_step()
+            for l in range(n_layers):
+                batch.attention(l, qs[l], kns[l], vns[l], softmax_scale=scale, n_rep=n_rep)
+            batch.end_step()
+        return step
 
-    fused_ms, _ = event_time_ms(step_fused, args.steps, args.warmup)
+    times = {k: [] for k in batches}
+    half = max(1, args.steps // 2)
+    for rnd in range(2):
+        for name in (("append_then_decode", "fused_append") if rnd == 0 else ("fused_append", "append_then_decode")):
+            ms, _ = event_time_ms(make_step(batches[name]), half, args.warmup if rnd == 0 else 1)
+            times[name].append(ms)
+    default_ms = sum(times["append_then_decode"]) / 2
+    fused_ms = sum(times["fused_append"]) / 2
     mean_len = float(np.mean([np.mean(x) for x in lens_log])) + 1.0
-    log(f"[bench] step fused: {fused_ms * 1e3:.1f} us")
-
-    # (b) prologue + append kernel + decode per layer
-    unfused = DecodeBatch(pool, [list(x) for x in lists0], lens0)
-
-    def step_unfused():
-        bt, attn = unfused.begin_step()
-        for l in range(n_layers):
-            unfused.append(l, kns[l], vns[l])
-            page16_native.page16_decode_attention(qs[l], pool.k_cache[l], pool.v_cache[l], bt, attn,
-                                                  softmax_scale=scale, n_rep=n_rep)
-        unfused.end_step()
-
-    unfused_ms, _ = event_time_ms(step_unfused, args.steps, args.warmup)
-    log(f"[bench] step unfused: {unfused_ms * 1e3:.1f} us")
+    log(f"[bench] step append-then-decode: {default_ms * 1e3:.1f} us, fused append: {fused_ms * 1e3:.1f} us")
+    fused = batches["fused_append"]
 
     # (c) the reference's call pattern with this build's decode kernel
     ref_lists = [list(x) for x in lists0]
@@ -410,16 +410,16 @@ def run_step(args, dev):
     max_blocks = int(fused.block_table.shape[1])
     layer_bytes = workloads.decode_bytes(np.full(B, mean_len), B, Hq, Hkv, D, max_blocks) + 2 * B * Hkv * D * 2
     step_bytes = n_layers * layer_bytes
-    gbps = step_bytes / (fused_ms * 1e-3) / 1e9
+    gbps = step_bytes / (default_ms * 1e-3) / 1e9
     name = "config3_ragged" if ragged else "config2_longctx"
     return {
-        "metric": f"Decode step over 32 layers (prologue + fused append/decode), {name}, tokens/s",
-        "value": round(B / (fused_ms * 1e-3), 1),
+        "metric": f"Decode step over 32 layers (prologue + append + decode per layer), {name}, tokens/s",
+        "value": round(B / (default_ms * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": 2 * half,
         "warmup": args.warmup,
-        "ms_per_step": round(fused_ms, 5),
+        "ms_per_step": round(default_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -428,9 +428,9 @@ def run_step(args, dev):
         "config": {"workload": f"decode_step_32_layers_{name}", "layers": n_layers, "batch": B,
                    "start_lengths_mean": float(np.mean(lens0)), "num_q_heads": Hq, "num_kv_heads": Hkv,
                    "head_dim": D, "page_size": 16, "pool_pages_per_layer": N},
-        "us_per_step": {"fused": round(fused_ms * 1e3, 1), "unfused_append_then_decode": round(unfused_ms * 1e3, 1),
+        "us_per_step": {"append_then_decode": round(default_ms * 1e3, 1), "fused_append": round(fused_ms * 1e3, 1),
                         "reference_call_pattern": round(ref_ms * 1e3, 1)},
-        "us_per_layer_saved_vs_reference_pattern": round((ref_ms - fused_ms) * 1e3 / n_layers, 2),
+        "us_per_layer_saved_vs_reference_pattern": round((ref_ms - default_ms) * 1e3 / n_layers, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
                      "note": "whole step: 32 x (KV pages read + token rows written) / step time"},

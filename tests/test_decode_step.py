@@ -169,8 +169,9 @@ def _assert_close(actual, expected, what):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fused_append", [False, True])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
-def test_multi_step_multi_layer_matches_reference_flow(cuda, dtype):
+def test_multi_step_multi_layer_matches_reference_flow(cuda, dtype, fused_append):
     from unifiedkv_amd.decode_step import DecodeBatch
 
     rng = np.random.default_rng(11)
@@ -196,7 +197,8 @@ def test_multi_step_multi_layer_matches_reference_flow(cuda, dtype):
     tokens = [[(_rand_bits(rng, (B, Hq, D), dtype), _rand_bits(rng, (B, Hkv, D), dtype),
                 _rand_bits(rng, (B, Hkv, D), dtype)) for _ in range(n_layers)] for _ in range(steps)]
 
-    batch = DecodeBatch(pool, lists, lens0, capacity_blocks=1)  # width 64: no growth needed here
+    batch = DecodeBatch(pool, lists, lens0, capacity_blocks=1,  # width 64: no growth needed here
+                        fused_append=fused_append)
     got = []
     for s in range(steps):
         batch.begin_step()
@@ -357,7 +359,8 @@ def test_exhaustion_keeps_earlier_pages_in_the_device_table(cuda):
 
 
 @pytest.mark.gpu
-def test_layer_calls_replay_from_a_captured_graph(cuda):
+@pytest.mark.parametrize("fused_append", [False, True])
+def test_layer_calls_replay_from_a_captured_graph(cuda, fused_append):
     # The per-layer fused append + decode calls of a step hold no host synchronisation and
     # no memset, so a serving loop can capture them. Capture one step's layers, then replay
     # the graph several times with eager work in between: every replay must equal the eager
@@ -372,7 +375,7 @@ def test_layer_calls_replay_from_a_captured_graph(cuda):
     pool.k_cache.copy_(_dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda))
     pool.v_cache.copy_(_dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda))
     lists = [pool.allocate_blocks(max(1, -(-L // 16))) for L in lens0]
-    batch = DecodeBatch(pool, lists, lens0)
+    batch = DecodeBatch(pool, lists, lens0, fused_append=fused_append)
     scale = 1.0 / math.sqrt(D)
     ins = [tuple(_dev(_rand_bits(rng, shape, dtype), dtype, cuda) for shape in ((B, Hq, D), (B, Hkv, D), (B, Hkv, D)))
            for _ in range(n_layers)]

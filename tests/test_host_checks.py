@@ -107,3 +107,8 @@ def test_prefill_write_rejects_out_of_range_layers():
     for bad in (-1, 2, 7):
         with pytest.raises(IndexError, match="outside the pool"):
             pp.write(bad, None, None)
+
+
+def test_decode_batch_rejects_pages_shared_between_sequences():
+    with pytest.raises(ValueError, match="more than one sequence"):
+        DecodeBatch(_FakePool(), [[1, 2], [3, 2]], [20, 20])
