@@ -32,6 +32,10 @@
  *   ukv_kv_write_varlen    core/pool.py:127-141 for a prefill chunk appended after its prefix
  *   ukv_paged_prefill      core/engine.py:1826-1854 chunked prefill attention over past KV
  *                          (HF attention / core/varlen.py:19-42 flash_attn_varlen_func, causal)
+ *   ukv_paged_prefill_obs_stats  that attention, also producing the observation window's
+ *                          softmax normalisers (core/scheduler.py:269-341 q-tail capture +
+ *                          the first half of core/scheduler.py:565-592)
+ *   ukv_snapkv_scores_from_stats  ukv_snapkv_scores taking those normalisers
  */
 #ifndef UKV_H_
 #define UKV_H_
@@ -311,6 +315,34 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
                       float softmax_scale, int dtype, ukv_stream_t stream);
 
 /*
+ * ukv_paged_prefill, and for the chunk's last obs_len queries of every sequence also SnapKV's
+ * row statistics over that sequence's middle keys (what ukv_snapkv_scores' first pass computes
+ * when the chunk is the sequence's last, L = kv_lens[b]): for q head h and window query i
+ * (chunk row C_b - obs_len + i),
+ *   obs_stats[2 * (b * stats_seq_stride + h * obs_len + i)]     = log2 of the sum over keys
+ *       j in [sink_len, L - obs_len), and the zero rows padding them to a multiple of 16, of
+ *       2^(q.k_j * softmax_scale * log2(e)) (a zero row scores 0);
+ *   obs_stats[2 * (b * stats_seq_stride + h * obs_len + i) + 1] = 0, or 1 where that sum fell
+ *       below 2^-100 of the query's largest weight (its low bits are lost; ukv_snapkv_scores_from_stats
+ *       recomputes such items).
+ * stats_seq_stride counts (value, flag) pairs and is at least num_q_heads * obs_len; obs_stats is
+ * 8-byte aligned. For the layout ukv_snapkv_scores_from_stats reads ([seqs][layers][num_q_heads]
+ * [obs_len] pairs) pass obs_stats + 2 * layer * num_q_heads * obs_len and stats_seq_stride =
+ * layers * num_q_heads * obs_len. Needs the tiled path (head_dim 128, n_rep 1/2/4/8/16, 16-byte
+ * aligned rows: UKV_ERR_INVALID_ARGUMENT otherwise) and C_b >= obs_len for the rows to exist.
+ * The reference captures the window's queries in its q_proj hook (core/scheduler.py:269-341)
+ * and normalises their softmax over K_mid at selection time (core/scheduler.py:565-592,
+ * core/compress.py:116-130); here that normaliser is taken while the prefill streams the keys.
+ */
+int ukv_paged_prefill_obs_stats(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                                const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch,
+                                int total_q, int max_chunk, int num_q_heads, int num_kv_heads, int head_dim,
+                                int n_rep, int max_blocks, int num_pages, const int64_t* q_strides,
+                                const int64_t* k_strides, const int64_t* v_strides, float softmax_scale, int dtype,
+                                int sink_len, int obs_len, float* obs_stats, int64_t stats_seq_stride,
+                                ukv_stream_t stream);
+
+/*
  * SnapKV observation-window block scores (the importance scores ukv_select_topk ranks).
  * For every item (layer l of sequence b, item = b * layers + l), with L = seq_len:
  *   K_mid = K[:, sink_len : L - obs_len, :] zero-padded to aligned = ceil(L_mid / block_size)
@@ -342,6 +374,20 @@ int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, const void* k
                       int sink_len, int obs_len, int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
                       int block_size, float softmax_scale, int dtype, float* scores, int64_t scores_stride,
                       void* workspace, size_t workspace_bytes, ukv_stream_t stream);
+
+/*
+ * ukv_snapkv_scores with the row statistics given: obs_stats holds [items][num_q_heads][obs_len]
+ * (value, flag) float pairs as ukv_paged_prefill_obs_stats writes them (8-byte aligned), so the
+ * first pass over the keys runs only for items with a flagged or non-finite row. Same scores up
+ * to the statistics' rounding; same arguments and workspace otherwise. Replaces, with
+ * ukv_paged_prefill_obs_stats, the same steps as ukv_snapkv_scores (core/scheduler.py:565-592).
+ */
+int ukv_snapkv_scores_from_stats(const void* q_obs, const int64_t* q_strides, const void* k,
+                                 const int64_t* k_strides, const int32_t* block_table, int max_blocks, int num_pages,
+                                 int layers, int seqs, int seq_len, int sink_len, int obs_len, int num_q_heads,
+                                 int num_kv_heads, int head_dim, int n_rep, int block_size, float softmax_scale,
+                                 int dtype, const float* obs_stats, float* scores, int64_t scores_stride,
+                                 void* workspace, size_t workspace_bytes, ukv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,9 @@ in float64 on host arrays:
                                     max over heads -> sum per block -> maxpool(3, 1, 1) if N >= 3
 * ``score_layer_blocks_loops``      the same with explicit loops (tiny shapes; cross-check)
 * ``maxpool3``            torch.nn.functional.max_pool1d(kernel_size=3, stride=1, padding=1)
+* ``obs_row_stats``       :586-587  the softmax's normaliser per (q head, query): log2 of
+                          sum_j exp(Q_obs K_mid_j^T * scale) over the padded K_mid, the row statistics
+                          ukv_paged_prefill_obs_stats produces during the prefill
 * ``score_heads_f32``     the dense fp32 formulation (matmul, softmax, mean) for a subset of heads:
                           the CPU baseline's sample
 * ``score_layer_blocks_model_dtype``  the same steps with the reference's rounding points: every
@@ -67,6 +70,21 @@ def score_layer_blocks(K, Q_obs, *, sink_len: int, obs_len: int, n_rep: int, blo
     s = A.mean(axis=1).max(axis=0)                      # [aligned]
     blocks = s.reshape(N, block_size).sum(axis=-1)
     return maxpool3(blocks) if N >= 3 else blocks
+
+
+def obs_row_stats(K, Q_obs, *, sink_len: int, obs_len: int, n_rep: int, block_size: int = 16,
+                  scale: float = None) -> np.ndarray:
+    """K [H_kv, L, D], Q_obs [H_q, obs, D] -> float64 [H_q, obs]: log2 sum_j 2^(s_j * scale * log2 e)
+    over the zero-padded middle keys j (the softmax normaliser of :586-587 in log2 units)."""
+    K = np.asarray(K, dtype=np.float64)
+    Q = np.asarray(Q_obs, dtype=np.float64)
+    scale = K.shape[2] ** -0.5 if scale is None else scale
+    K_mid, N = mid_keys(K, sink_len, obs_len, block_size)
+    if N == 0:
+        return np.empty((Q.shape[0], 0))
+    S = np.matmul(Q, repeat_kv(K_mid, n_rep).transpose(0, 2, 1)) * scale  # natural-log units
+    m = S.max(axis=-1, keepdims=True)
+    return (m[..., 0] + np.log(np.exp(S - m).sum(axis=-1))) / math.log(2.0)
 
 
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:

@@ -1,0 +1,284 @@
+"""SnapKV's softmax normalisers taken during the prefill, and the scores that start from them.
+
+The reference captures the observation window's queries in its q_proj hook during the prefill
+(core/scheduler.py:269-341) and, at selection time, normalises their softmax over the middle
+keys K_mid (core/scheduler.py:565-592). ``ukv_paged_prefill_obs_stats`` takes that
+normaliser (log2 sum_j 2^(s_j * scale * log2 e) over the zero-padded K_mid) while the prefill
+kernel streams the keys, and ``ukv_snapkv_scores_from_stats`` skips its own pass over the keys.
+
+Checked here:
+* the oracle's normaliser (snapkv_oracle.obs_row_stats) against scipy's logsumexp, against
+  the closed form for all-zero keys (log2 of the padded key count) and against the oracle's
+  own scores (weights 2^(s - lse) sum to 1 per row, and rebuild score_layer_blocks);
+* on the GPU, the prefill's rows against that oracle (fp64) within LSE_TOL in log2 units
+  (the rows are fp32 sums of fp32 weights), its attention output
+  against the plain prefill's, the scores from these rows against the two-pass scores
+  (within the two-pass first pass's own rounding: each weight enters its sum as fp16,
+  2^-11 relative) and against the fp64 oracle with the bound the other score tests use;
+* rows the kernel flags (a sum that underflowed because the sink dominates) and rows that
+  are flagged or non-finite in the given statistics: those items are recomputed by the
+  first pass and then equal the two-pass scores bit for bit;
+* the host-side refusals (chunk shorter than the window, a layer not written, another
+  length or softmax scale).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from oracle import snapkv_oracle as so
+from unifiedkv_amd import workloads
+
+LSE_TOL = 5e-6   # log2 units: relative error of the normaliser <= 3.5e-6 (measured worst 2.0e-6)
+
+
+def _rand(rng, shape):
+    return rng.standard_normal(shape)
+
+
+def test_oracle_normaliser_matches_scipy_logsumexp():
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(3)
+    Hkv, n_rep, L, D, sink, obs = 2, 3, 203, 32, 5, 24
+    K, Q = _rand(rng, (Hkv, L, D)), _rand(rng, (Hkv * n_rep, obs, D))
+    scale = 0.37
+    got = so.obs_row_stats(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep, scale=scale)
+    L_mid = L - sink - obs
+    aligned = -(-L_mid // 16) * 16
+    for h in range(Hkv * n_rep):
+        Km = np.concatenate([K[h // n_rep, sink:L - obs], np.zeros((aligned - L_mid, D))])
+        want = logsumexp(Q[h] @ Km.T * scale, axis=-1) / math.log(2.0)
+        np.testing.assert_allclose(got[h], want, rtol=0, atol=1e-12)
+
+
+def test_oracle_normaliser_of_zero_keys_is_log2_of_the_padded_count():
+    K = np.zeros((1, 101, 8))
+    Q = np.ones((2, 16, 8))
+    got = so.obs_row_stats(K, Q, sink_len=4, obs_len=16, n_rep=2)
+    np.testing.assert_allclose(got, math.log2(96), rtol=1e-15)  # 81 middle keys padded to 96, scores 0
+
+
+def test_oracle_normaliser_rebuilds_the_oracle_scores():
+    rng = np.random.default_rng(4)
+    Hkv, n_rep, L, D, sink, obs = 2, 2, 330, 16, 16, 32
+    K, Q = _rand(rng, (Hkv, L, D)), _rand(rng, (Hkv * n_rep, obs, D))
+    lse = so.obs_row_stats(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep)
+    K_mid, N = so.mid_keys(K, sink, obs, 16)
+    S = Q @ so.repeat_kv(K_mid, n_rep).transpose(0, 2, 1) * (D ** -0.5) / math.log(2.0)
+    A = np.exp2(S - lse[..., None])
+    np.testing.assert_allclose(A.sum(-1), 1.0, rtol=0, atol=1e-12)
+    blocks = A.mean(axis=1).max(axis=0).reshape(N, 16).sum(-1)
+    want = so.score_layer_blocks(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep)
+    np.testing.assert_allclose(so.maxpool3(blocks), want, rtol=1e-12, atol=0)
+
+
+def test_obs_stats_host_checks():
+    import torch
+
+    from unifiedkv_amd import snapkv
+    from unifiedkv_amd.prefill import paged_prefill_attention
+
+    st = snapkv.ObsStats(2, 3, 8, sink_len=4, obs_len=32, softmax_scale=0.125, device="meta")
+    assert st.layer_view(2)[1] == 3 * 8 * 32
+    with pytest.raises(IndexError):
+        st.layer_view(3)
+    meta = torch.device("meta")
+    q = torch.empty((100, 8, 128), dtype=torch.bfloat16, device=meta)
+    kc = torch.empty((40, 16, 2, 128), dtype=torch.bfloat16, device=meta)
+    bt = torch.empty((2, 10), dtype=torch.int32, device=meta)
+    call = dict(softmax_scale=0.125, n_rep=4, obs_stats=st, layer_id=0)
+    with pytest.raises(RuntimeError, match="obs_window_spans_chunks"):
+        paged_prefill_attention(q, kc, kc, bt, [0, 80, 100], [150, 120], **call)
+    with pytest.raises(RuntimeError, match="obs_stats_scale"):
+        paged_prefill_attention(q, kc, kc, bt, [0, 50, 100], [150, 120], **dict(call, softmax_scale=0.1))
+    with pytest.raises(ValueError, match="needs layer_id"):
+        paged_prefill_attention(q, kc, kc, bt, [0, 50, 100], [150, 120], **dict(call, layer_id=None))
+    with pytest.raises(RuntimeError, match="paged_prefill_unavailable:device"):
+        paged_prefill_attention(q, kc, kc, bt, [0, 50, 100], [150, 120], **call)
+    # score side: every layer written at the scored length, same window and scale
+    check = dict(seqs=2, layers=3, h_q=8, seq_len=150, sink_len=4, obs_len=32, scale=0.125, dev=meta)
+    with pytest.raises(RuntimeError, match="layer_missing"):
+        snapkv._check_obs_stats(st, **check)
+    for layer in range(3):
+        st.mark(layer, [150, 150])
+    assert snapkv._check_obs_stats(st, **check) is st.data
+    with pytest.raises(RuntimeError, match="seq_len"):
+        snapkv._check_obs_stats(st, **dict(check, seq_len=151))
+    with pytest.raises(RuntimeError, match="softmax_scale"):
+        snapkv._check_obs_stats(st, **dict(check, scale=0.1))
+    with pytest.raises(RuntimeError, match="bad_score_shape:obs_stats"):
+        snapkv._check_obs_stats(st, **dict(check, obs_len=16))
+
+
+# --------------------------------------------------------------------------- GPU
+
+
+def _bits(rng, shape, dtype):
+    return workloads._round_bits(rng.standard_normal(shape, dtype=np.float32), dtype)
+
+
+def _dev(bits, dtype):
+    import torch
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to("cuda").view(tdt)
+
+
+def _f(bits, dtype):
+    return oracle.bits_to_f32(bits, workloads.DTYPE_CODES[dtype])
+
+
+def _prefill(cuda, dtype, chunks, *, Hq, Hkv, layers, sink, obs, seed, q_fill=None, k_sink_fill=None):
+    """Chunked prefill through PrefillPages, the final chunk with ObsStats; returns what the
+    checks need: pool, pages, statistics, the final chunk's outputs with and without them,
+    the window's queries and the dense keys."""
+    import torch
+
+    from unifiedkv_amd import snapkv
+    from unifiedkv_amd.pool import PagedKVPool
+    from unifiedkv_amd.prefill import PrefillPages, paged_prefill_attention
+
+    rng = np.random.default_rng(seed)
+    D = 128
+    n_rep = Hq // Hkv
+    scale = 1.0 / math.sqrt(D)
+    B = len(chunks[0])
+    total_len = [sum(c[b] for c in chunks) for b in range(B)]
+    pool = PagedKVPool(16, layers, Hkv, D, torch.bfloat16 if dtype == "bf16" else torch.float16,
+                       num_blocks=sum(-(-n // 16) for n in total_len) + 8, device=cuda)
+    pool.allocate_blocks(3)                      # pages of the prefill do not start at 0
+    pp = PrefillPages(pool, B)
+    st = snapkv.ObsStats(B, layers, Hq, sink_len=sink, obs_len=obs, softmax_scale=scale, device=cuda)
+    q_obs = np.zeros((B, layers, Hq, obs, D), np.uint16)
+    outs = {}
+    for ci, cl in enumerate(chunks):
+        last = ci == len(chunks) - 1
+        pp.begin_chunk(cl)
+        total = sum(cl)
+        cu = np.concatenate([[0], np.cumsum(cl)]).astype(np.int64)
+        for layer in range(layers):
+            q, k, v = (_bits(rng, (total, Hq, D), dtype), _bits(rng, (total, Hkv, D), dtype),
+                       _bits(rng, (total, Hkv, D), dtype))
+            if q_fill is not None:
+                q[:] = workloads._round_bits(np.full(q.shape, q_fill, np.float32), dtype)
+            if k_sink_fill is not None and ci == 0:
+                k[cu[:-1]] = workloads._round_bits(np.full((B, Hkv, D), k_sink_fill, np.float32), dtype)
+            if last:
+                out = pp.attention(layer, _dev(q, dtype), _dev(k, dtype), _dev(v, dtype), softmax_scale=scale,
+                                   n_rep=n_rep, obs_stats=st)
+                c = pp._chunk
+                plain = paged_prefill_attention(_dev(q, dtype), pool.k_cache[layer], pool.v_cache[layer], c["bt"],
+                                                c["cu"], c["kv"], softmax_scale=scale, n_rep=n_rep,
+                                                max_chunk=c["max_chunk"])
+                outs[layer] = (out.float().cpu().numpy(), plain.float().cpu().numpy())
+                for b in range(B):
+                    q_obs[b, layer] = q[cu[b + 1] - obs:cu[b + 1]].transpose(1, 0, 2)
+            else:
+                pp.attention(layer, _dev(q, dtype), _dev(k, dtype), _dev(v, dtype), softmax_scale=scale,
+                             n_rep=n_rep)
+        pp.end_chunk()
+    torch.cuda.synchronize()
+    dense = []
+    for layer in range(layers):
+        kc = pool.k_cache[layer].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        dense.append([kc[np.asarray(pp.page_lists[b])].reshape(-1, Hkv, D)[:total_len[b]].transpose(1, 0, 2)
+                      for b in range(B)])
+    return dict(pool=pool, pp=pp, st=st, outs=outs, q_obs=q_obs, dense=dense, scale=scale, n_rep=n_rep,
+                lens=total_len, D=D)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype, Hq, Hkv, sink, obs, chunks", [
+    ("bf16", 16, 4, 4, 32, [[700, 650], [400, 517]]),
+    ("fp16", 16, 2, 64, 128, [[900, 300], [300, 901]]),
+    ("bf16", 8, 8, 0, 48, [[1000, 500], [300, 48]]),  # n_rep 1, obs not a multiple of 16, no sink,
+                                                      # a final chunk of exactly the window
+    ("bf16", 32, 8, 16, 128, [[300, 2000]]),          # one chunk each
+])
+def test_prefill_rows_match_oracle_and_outputs_match_plain_prefill(cuda, dtype, Hq, Hkv, sink, obs, chunks):
+    layers = 2
+    r = _prefill(cuda, dtype, chunks, Hq=Hq, Hkv=Hkv, layers=layers, sink=sink, obs=obs, seed=7)
+    data = r["st"].data.cpu().numpy()
+    worst = 0.0
+    for layer in range(layers):
+        out, plain = r["outs"][layer]
+        ok, err, exc = oracle.allclose_report(out, plain, 2e-3, 1e-2)
+        assert ok, f"layer {layer}: output differs from the plain prefill by {err:.3e}"
+        for b in range(len(chunks[0])):
+            want = so.obs_row_stats(_f(r["dense"][layer][b], dtype), _f(r["q_obs"][b, layer], dtype), sink_len=sink,
+                                    obs_len=obs, n_rep=r["n_rep"], scale=r["scale"])
+            got = data[b, layer, :, :, 0]
+            assert np.all(data[b, layer, :, :, 1] == 0), "no row should be flagged here"
+            err = np.abs(got - want).max()
+            worst = max(worst, err)
+            assert err <= LSE_TOL, f"layer {layer} seq {b}: normaliser off by {err:.3e} (log2 units)"
+    print(f"max |lse - oracle| = {worst:.3e}")
+
+
+def _scores(r, *, sink, obs, stats):
+    import torch
+
+    from unifiedkv_amd import snapkv
+
+    pp = r["pp"]
+    width = max(len(x) for x in pp.page_lists)
+    table = torch.tensor([x + [0] * (width - len(x)) for x in pp.page_lists], dtype=torch.int32, device="cuda")
+    q_obs = r["q_dev"]
+    return snapkv.score_blocks(q_obs, r["pool"].k_cache, table, seq_len=r["lens"][0], sink_len=sink, obs_len=obs,
+                               n_rep=r["n_rep"], obs_stats=r["st"] if stats else None)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_scores_from_prefill_rows_match_two_pass_and_oracle(cuda, dtype):
+    sink, obs, layers = 16, 64, 3
+    r = _prefill(cuda, dtype, [[1500, 1500], [613, 613]], Hq=16, Hkv=4, layers=layers, sink=sink, obs=obs, seed=11)
+    r["q_dev"] = _dev(r["q_obs"], dtype)
+    one = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
+    # the first pass's weights enter its normaliser as fp16 (2^-11 relative each), and the
+    # second pass rounds its weights to fp16 under either normaliser
+    np.testing.assert_allclose(one, two, rtol=2.0 ** -9, atol=1e-7)
+    for b in range(2):
+        for layer in range(layers):
+            want = so.score_layer_blocks(_f(r["dense"][layer][b], dtype), _f(r["q_obs"][b, layer], dtype),
+                                         sink_len=sink, obs_len=obs, n_rep=r["n_rep"])
+            got = one[b * layers + layer]
+            err = np.abs(got - want)
+            assert np.all(err <= 1e-4 * np.abs(want).max() + 1e-3 * np.abs(want)), (b, layer, err.max())
+
+
+@pytest.mark.gpu
+def test_flagged_or_non_finite_rows_make_the_first_pass_redo_their_items(cuda):
+    sink, obs, layers = 4, 32, 2
+    r = _prefill(cuda, "bf16", [[800, 800], [300, 300]], Hq=16, Hkv=4, layers=layers, sink=sink, obs=obs, seed=5)
+    r["q_dev"] = _dev(r["q_obs"], "bf16")
+    clean = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
+    data = r["st"].data
+    data[1, 0, 3, 5, 0] = 1e30                    # a wrong value, flagged: item (seq 1, layer 0)
+    data[1, 0, 3, 5, 1] = 1.0
+    data[0, 1, 0, 0, 0] = float("nan")            # non-finite, unflagged: item (seq 0, layer 1)
+    got = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    redone = [1 * layers + 0, 0 * layers + 1]
+    for item in range(2 * layers):
+        want = two[item] if item in redone else clean[item]
+        assert np.array_equal(got[item], want), item
+
+
+@pytest.mark.gpu
+def test_a_dominant_sink_flags_the_rows_and_the_scores_stay_exact(cuda):
+    # every query is (1, ..., 1) and the first key of each sequence is (16, ..., 16): its score
+    # 2048 / sqrt(128) = 181 sits 261 log2 units above the middle keys', whose weights under
+    # that max underflow fp32 - the kernel flags every window row, and the scores recompute them
+    sink, obs, layers = 4, 32, 1
+    r = _prefill(cuda, "bf16", [[600, 600]], Hq=8, Hkv=2, layers=layers, sink=sink, obs=obs, seed=9, q_fill=1.0,
+                 k_sink_fill=16.0)
+    flags = r["st"].data[..., 1].cpu().numpy()
+    assert np.all(flags == 1.0)
+    r["q_dev"] = _dev(r["q_obs"], "bf16")
+    one = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
+    assert np.array_equal(one, two)

@@ -152,6 +152,16 @@ SIGNATURES = {
             ctypes.c_float, _c_int, _c_void_p,  # scale dtype stream
         ],
     ),
+    "ukv_paged_prefill_obs_stats": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q k v bt cu kv_lens out
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,  # batch total_q max_chunk Hq Hkv D n_rep
+            _c_int, _c_int, _c_i64p, _c_i64p, _c_i64p,  # max_blocks num_pages strides
+            ctypes.c_float, _c_int,  # scale dtype
+            _c_int, _c_int, _c_void_p, ctypes.c_int64, _c_void_p,  # sink obs stats stats_seq_stride stream
+        ],
+    ),
     "ukv_snapkv_block_count": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "ukv_snapkv_workspace_bytes": (
         ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -163,6 +173,18 @@ SIGNATURES = {
             _c_int, _c_int, _c_int, _c_int, _c_int,  # layers, seqs, seq_len, sink, obs
             _c_int, _c_int, _c_int, _c_int, _c_int,  # Hq, Hkv, D, n_rep, block_size
             ctypes.c_float, _c_int, _c_void_p, ctypes.c_int64,  # scale, dtype, scores, stride
+            _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
+        ],
+    ),
+    "ukv_snapkv_scores_from_stats": (
+        _c_int,
+        [
+            _c_void_p, _c_i64p, _c_void_p, _c_i64p,  # q_obs, strides, k, strides
+            _c_void_p, _c_int, _c_int,  # block_table, max_blocks, num_pages
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # layers, seqs, seq_len, sink, obs
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # Hq, Hkv, D, n_rep, block_size
+            ctypes.c_float, _c_int, _c_void_p,  # scale, dtype, obs_stats
+            _c_void_p, ctypes.c_int64,  # scores, stride
             _c_void_p, ctypes.c_size_t, _c_void_p,  # workspace, bytes, stream
         ],
     ),

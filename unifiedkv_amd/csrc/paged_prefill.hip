@@ -57,6 +57,14 @@ struct PrefillArgs {
   const int32_t* kv_lens;  // [B] keys per sequence, the chunk included
   int B, Hq, n_rep, n_groups, D, max_blocks, num_pages, n_qblocks;
   float scale, scale_log2;
+  // SnapKV observation statistics (obs > 0): the query blocks that hold a sequence's last obs
+  // queries run in the STATS instance, which also writes, for each of those queries and q head
+  // h, the log2-sum-exp2 of its scaled scores over the middle keys [sink, L - obs) and the zero
+  // rows that pad them to a multiple of 16 keys: obs_stats[b * stats_seq_stride + h * obs + i].x
+  // (.y = 0, or 1 where the sum lost precision), the row statistics the SnapKV scoring pass takes.
+  float2* obs_stats;
+  int64_t stats_seq_stride;
+  int sink, obs, n_obs_blocks, n_stats_wgs;
 };
 
 __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
@@ -154,19 +162,28 @@ __device__ void prefill_pairs_fp32(const PrefillArgs& a, int b, int g, int q_beg
   }
 }
 
-template <int DT, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
-paged_prefill_kernel(const PrefillArgs a) {
+// LDS of one workgroup: kStages ring slots of K and V (fp16) tiles.
+struct PrefillLds {
+  __attribute__((aligned(16))) uint16_t k_s[kStages][kTileKeys][kRowPad];
+  __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kVRowPad];
+};
+
+// Workgroup wg of the tiled prefill. STATS: the workgroups of the query blocks that hold the
+// sequences' last obs queries (two column blocks per wave), which also produce those queries'
+// SnapKV row statistics.
+template <int DT, int WAVES, bool STATS>
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg, PrefillLds& lds) {
   constexpr int D = 128;
   constexpr int STEPS = D / 32;
   constexpr int NT = 64 * WAVES;
   constexpr int ITEMS = kTileKeys * 16 / NT;  // 16-byte chunks per thread per tensor per tile
-  constexpr int CB = kColBlocks;
+  // The STATS instance holds two column blocks, which leaves registers for its sums.
+  constexpr int CB = STATS ? 2 : kColBlocks;
   constexpr float kTau = 8.f;
   constexpr bool kBf16 = DT == UKV_DTYPE_BF16;
   static_assert(ITEMS * NT == kTileKeys * 16, "loader mapping");
-  __shared__ __attribute__((aligned(16))) uint16_t k_s[kStages][kTileKeys][kRowPad];
-  __shared__ __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kVRowPad];  // fp16
+  auto& k_s = lds.k_s;
+  auto& v_s = lds.v_s;  // fp16
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -174,22 +191,37 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int i16 = lane & 15;
   const int kg = lane >> 4;
 
-  // Work item of this workgroup: each XCD takes a contiguous range.
-  const int n_qb = a.n_qblocks;
-  const int total = n_qb * a.n_groups * a.B;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int per = total >> 3, rem = total & 7;
-  const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
-  const int qblk = n_qb - 1 - work % n_qb;  // the longest query blocks of a group first
-  const int g = (work / n_qb) % a.n_groups;
-  const int b = work / (n_qb * a.n_groups);
-
   const int qpb = 16 / a.n_rep;  // queries per column block
   const int qw = WAVES * CB * qpb;
+  // Queries from obs_q0(C) on run in the STATS instance when obs > 0: the main instance's
+  // query blocks from the one holding query C - obs.
+  const int qw_main = WAVES * kColBlocks * qpb;
+  auto obs_q0 = [&](int Cq) { return max(0, Cq - a.obs) / qw_main * qw_main; };
+  int q0, g, b;
+  if constexpr (STATS) {
+    const int j = wg % a.n_obs_blocks;
+    g = (wg / a.n_obs_blocks) % a.n_groups;
+    b = wg / (a.n_obs_blocks * a.n_groups);
+    if (b >= a.B) return;  // the count is rounded up to a multiple of 8
+    q0 = obs_q0(a.cu_q[b + 1] - a.cu_q[b]) + j * qw;
+  } else {
+    int qblk;
+    // Work item of this workgroup: each XCD takes a contiguous range.
+    const int n_qb = a.n_qblocks;
+    const int total = n_qb * a.n_groups * a.B;
+    const int xcd = wg & 7, slot = wg >> 3;
+    const int per = total >> 3, rem = total & 7;
+    const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+    qblk = n_qb - 1 - work % n_qb;  // the longest query blocks of a group first
+    g = (work / n_qb) % a.n_groups;
+    b = work / (n_qb * a.n_groups);
+    q0 = qblk * qw;
+  }
   const int q_begin = a.cu_q[b];
   const int C = a.cu_q[b + 1] - q_begin;
-  const int q0 = qblk * qw;
   if (q0 >= C) return;  // whole workgroup
+  if constexpr (!STATS)
+    if (a.obs > 0 && q0 >= obs_q0(C)) return;  // the STATS instance's queries
   const int Lk = kv_len_of(a, b);
   const int P0 = Lk - C;  // keys before the chunk
   const int kend = max(0, min(Lk, P0 + min(C, q0 + qw)));
@@ -217,6 +249,12 @@ paged_prefill_kernel(const PrefillArgs a) {
   float m_ref[CB];  // running max of the column (log2 units)
   f32x4 o[CB][8];
   f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
+  // STATS: this lane's fp32 sum of 2^(s - m_ref) over its middle keys of column i16.
+  float lmid[STATS ? CB : 1];
+  const int mid_end = STATS ? Lk - a.obs : 0;
+  if constexpr (STATS)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) lmid[cb] = 0.f;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     m_ref[cb] = kNegFltMax;
@@ -342,6 +380,9 @@ paged_prefill_kernel(const PrefillArgs a) {
     // like their values, and inf and NaN lie above), and a column block whose
     // max moved is rescaled and its P recomputed.
     u32x4 pa[CB];
+    // STATS: is the tile's key kb*16 + 4kg + r one of the middle keys [sink, L - obs)?
+    const bool mid_all = STATS && key0 >= a.sink && key0 + kTileKeys <= mid_end;
+    const bool mid_none = !STATS || key0 + kTileKeys <= a.sink || key0 >= mid_end;
     auto exp_pack = [&](int cb) {
       float p[2][4];
 #pragma unroll
@@ -350,37 +391,61 @@ paged_prefill_kernel(const PrefillArgs a) {
         for (int r = 0; r < 4; ++r) p[kb][r] = fast_exp2(__builtin_fmaf(sacc[kb][cb][r], sl2, -m_ref[cb]));
       pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                      pack_f16(p[1][2], p[1][3])};
+      if constexpr (STATS) {
+        if (!mid_none) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int key = key0 + kb * 16 + 4 * kg + r;
+              lmid[cb] += (mid_all || (key >= a.sink && key < mid_end)) ? p[kb][r] : 0.f;
+            }
+        }
+      }
     };
+    // Moves column block cb's max to the tile's where that lies more than kTau above it,
+    // rescaling what was summed under the old one; returns whether it moved.
+    auto settle = [&](int cb) -> bool {
+      float mloc = sacc[0][cb][0];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) exp_pack(cb);
-    u16x2 pmax = as_u16x2(pa[0][0]);
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
+        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[kb][cb][r]);
+      float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
+      mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
+      if (!__any(mcol * sl2 > m_ref[cb] + kTau)) return false;
+      const float m_new = fmaxf(m_ref[cb], mcol * sl2);
+      const float alpha = fast_exp2(m_ref[cb] - m_new);
+      m_ref[cb] = m_new;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) pmax = __builtin_elementwise_max(pmax, as_u16x2(pa[cb][c]));
-    if (__any(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(pmax, u16x2{0x5BFF, 0x5BFF})) != 0u)) {
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * kg + r);
+        lacc[cb][r] *= ar;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
+      }
+      if constexpr (STATS) lmid[cb] *= alpha;  // lane-local: column i16, like m_ref
+      return true;
+    };
+    if constexpr (STATS) {
+      // The middle sums take every weight once, in fp32: settle the max before the weights.
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        float mloc = sacc[0][cb][0];
+        settle(cb);
+        exp_pack(cb);
+      }
+    } else {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int cb = 0; cb < CB; ++cb) exp_pack(cb);
+      u16x2 pmax = as_u16x2(pa[0][0]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[kb][cb][r]);
-        float mcol = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mcol = fmaxf(mcol, __shfl_xor(mcol, 32));
-        if (__any(mcol * sl2 > m_ref[cb] + kTau)) {
-          const float m_new = fmaxf(m_ref[cb], mcol * sl2);
-          const float alpha = fast_exp2(m_ref[cb] - m_new);
-          m_ref[cb] = m_new;
+      for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float ar = __shfl(alpha, 4 * kg + r);
-            lacc[cb][r] *= ar;
+        for (int c = 0; c < 4; ++c) pmax = __builtin_elementwise_max(pmax, as_u16x2(pa[cb][c]));
+      if (__any(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(pmax, u16x2{0x5BFF, 0x5BFF})) != 0u)) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
-          }
-          exp_pack(cb);
-        }
+        for (int cb = 0; cb < CB; ++cb)
+          if (settle(cb)) exp_pack(cb);
       }
     }
     // P.V: the B operand of output tile e (dims 16e .. 16e + 15) holds, in lane
@@ -446,6 +511,32 @@ paged_prefill_kernel(const PrefillArgs a) {
     vm_wait<0>(rk1[i], rv1[i]);
   }
 
+  if constexpr (STATS) {
+    // Row statistics of the observation queries: log2 of the sum over the middle keys and the
+    // n_pad zero rows (score 0) that pad them to whole 16-key blocks, in the units of
+    // s * scale * log2(e). Column i16 of each column block; the 4 lane groups hold its keys.
+    const int L_mid = Lk - a.sink - a.obs;
+    const int n_pad = ((L_mid + 15) & ~15) - L_mid;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      float l = lmid[cb] + __shfl_xor(lmid[cb], 16);
+      l += __shfl_xor(l, 32);
+      const int qi = wq0 + cb * qpb + i16 / a.n_rep;
+      const int hh = g * a.n_rep + i16 % a.n_rep;
+      if (wave_live && kg == 0 && qi >= C - a.obs && qi < C && hh < a.Hq) {
+        const float m = m_ref[cb];
+        const float top = n_pad > 0 ? fmaxf(m, 0.f) : m;
+        const float lse = top + __log2f(l * exp2f(m - top) + (float)n_pad * exp2f(-top));
+        // m is the max over every key the query sees, the sink and window included: middle
+        // weights below 2^-126 of it lose bits, so a sum under 2^-100 marks the row (y = 1)
+        // for the scoring pass to recompute from the keys.
+        const bool exact = l >= 0x1p-100f && __builtin_isfinite(lse);
+        a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)hh * a.obs + (qi - (C - a.obs))] =
+            make_float2(lse, exact ? 0.f : 1.f);
+      }
+    }
+  }
+
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
   if (kBf16 && __syncthreads_or(wide_mine)) {
@@ -470,6 +561,25 @@ paged_prefill_kernel(const PrefillArgs a) {
         for (int e = 0; e < 8; ++e) orow[16 * e] = Elem<DT>::from_float(o[cb][e][r] * inv);
       }
     }
+  }
+}
+
+// One launch: with WITH_STATS, workgroups 0 .. n_stats_wgs - 1 (a multiple of 8, so that
+// workgroup wg of the rest still runs on XCD wg % 8) are the STATS blocks - the longest of
+// every (sequence, group), dispatched first - and the rest the other query blocks.
+template <int DT, int WAVES, bool WITH_STATS>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+paged_prefill_kernel(const PrefillArgs a) {
+  __shared__ PrefillLds lds;
+  if constexpr (WITH_STATS) {
+    const int ns = a.n_stats_wgs;
+    if ((int)blockIdx.x < ns) {
+      prefill_tile<DT, WAVES, true>(a, blockIdx.x, lds);
+      return;
+    }
+    prefill_tile<DT, WAVES, false>(a, blockIdx.x - ns, lds);
+  } else {
+    prefill_tile<DT, WAVES, false>(a, blockIdx.x, lds);
   }
 }
 
@@ -685,12 +795,19 @@ extern "C" int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
 }
 
-extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
-                                 const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch,
-                                 int total_q, int max_chunk, int num_q_heads, int num_kv_heads, int head_dim,
-                                 int n_rep, int max_blocks, int num_pages, const int64_t* q_strides,
-                                 const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
-                                 int dtype, ukv_stream_t stream_handle) {
+namespace {
+
+struct ObsStats {
+  void* stats;
+  int64_t seq_stride;
+  int sink, obs;
+};
+
+int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                 const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch, int total_q, int max_chunk,
+                 int num_q_heads, int num_kv_heads, int head_dim, int n_rep, int max_blocks, int num_pages,
+                 const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
+                 int dtype, ukv_stream_t stream_handle, const ObsStats* obs) {
   if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0) return UKV_ERR_EMPTY;
   if (head_dim > 256) return UKV_ERR_HEAD_DIM;
   if (dtype != UKV_DTYPE_F16 && dtype != UKV_DTYPE_BF16) return UKV_ERR_DTYPE;
@@ -737,17 +854,39 @@ extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void*
                           in_page_ok(a.v_st, a.v_sh);
   const bool fast = head_dim == 128 && softmax_scale > 0.f && std::isfinite(softmax_scale) && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
                     strides_ok && al16(q) && al16(out) && al16(k_cache) && al16(v_cache) && max_blocks > 0;
+  if (obs) {
+    if (!fast) return UKV_ERR_INVALID_ARGUMENT;  // the statistics come from the tiled kernel only
+    a.obs_stats = static_cast<float2*>(obs->stats);
+    a.stats_seq_stride = obs->seq_stride;
+    a.sink = obs->sink;
+    a.obs = obs->obs;
+  }
   if (fast) {
     constexpr int W = UKV_PREFILL_WAVES;
     const int qw = W * kColBlocks * (16 / n_rep);
     a.n_qblocks = (max_chunk + qw - 1) / qw;
     const int64_t wgs = (int64_t)a.n_qblocks * n_groups * batch;
     if (wgs == 0) return UKV_OK;
-    if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
-    if (dtype == UKV_DTYPE_BF16)
-      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
-    else
-      hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+    if (!obs) {
+      if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
+      if (dtype == UKV_DTYPE_BF16)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+      else
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+    } else {
+      // The STATS blocks (2 column blocks per wave) cover queries obs_q0 .. C - 1, fewer
+      // than obs + qw of them.
+      const int qw_stats = W * 2 * (16 / n_rep);
+      a.n_obs_blocks = (a.obs + qw - 1 + qw_stats - 1) / qw_stats;
+      const int64_t swgs = ((int64_t)a.n_obs_blocks * n_groups * batch + 7) / 8 * 8;
+      if (swgs + wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
+      a.n_stats_wgs = (int)swgs;
+      const dim3 grid((unsigned)(swgs + wgs));
+      if (dtype == UKV_DTYPE_BF16)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), grid, dim3(64 * W), 0, stream, a);
+      else
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, true>), grid, dim3(64 * W), 0, stream, a);
+    }
   } else {
     const dim3 grid(total_q, num_q_heads);
     if (dtype == UKV_DTYPE_BF16)
@@ -756,4 +895,34 @@ extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void*
       hipLaunchKernelGGL(paged_prefill_scalar_kernel<UKV_DTYPE_F16>, grid, dim3(256), 0, stream, a);
   }
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                                 const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch,
+                                 int total_q, int max_chunk, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int n_rep, int max_blocks, int num_pages, const int64_t* q_strides,
+                                 const int64_t* k_strides, const int64_t* v_strides, float softmax_scale,
+                                 int dtype, ukv_stream_t stream_handle) {
+  return prefill_impl(q, k_cache, v_cache, block_table, cu_seqlens_q, kv_lens, out, batch, total_q, max_chunk,
+                      num_q_heads, num_kv_heads, head_dim, n_rep, max_blocks, num_pages, q_strides, k_strides,
+                      v_strides, softmax_scale, dtype, stream_handle, nullptr);
+}
+
+extern "C" int ukv_paged_prefill_obs_stats(const void* q, const void* k_cache, const void* v_cache,
+                                           const int32_t* block_table, const int32_t* cu_seqlens_q,
+                                           const int32_t* kv_lens, void* out, int batch, int total_q, int max_chunk,
+                                           int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                                           int max_blocks, int num_pages, const int64_t* q_strides,
+                                           const int64_t* k_strides, const int64_t* v_strides,
+                                           float softmax_scale, int dtype, int sink_len, int obs_len,
+                                           float* obs_stats, int64_t stats_seq_stride, ukv_stream_t stream_handle) {
+  if (sink_len < 0 || obs_len <= 0 || !obs_stats || (reinterpret_cast<uintptr_t>(obs_stats) & 7u) ||
+      stats_seq_stride < (int64_t)num_q_heads * obs_len)
+    return UKV_ERR_INVALID_ARGUMENT;
+  const ObsStats st{obs_stats, stats_seq_stride, sink_len, obs_len};
+  return prefill_impl(q, k_cache, v_cache, block_table, cu_seqlens_q, kv_lens, out, batch, total_q, max_chunk,
+                      num_q_heads, num_kv_heads, head_dim, n_rep, max_blocks, num_pages, q_strides, k_strides,
+                      v_strides, softmax_scale, dtype, stream_handle, &st);
 }

@@ -70,6 +70,7 @@ struct SnapArgs {
   float2* part_stats;    // [items][S][Hq*obs] (m, l) per range
   float2* stats;         // [items][Hq*obs] (m + log2(l), unused)
   float* raw;            // [items][n_blocks] block sums before pooling
+  int32_t* redo;         // [items] or null: pass 1 and the merge run only for items with redo != 0
   float* out;            // [items][out_stride]
   int64_t out_stride;
 };
@@ -144,6 +145,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int s = blockIdx.x, item = blockIdx.y;
+  if (!SCORES && a.redo && a.redo[item] == 0) return;  // whole workgroup: statistics given
   const int t0 = (int)((int64_t)s * a.Kt / a.S), t1 = (int)((int64_t)(s + 1) * a.Kt / a.S);
   const int key0 = t0 * kSnapTile;
   const int R = a.hp * a.obs;  // rows of a unit
@@ -455,6 +457,7 @@ __global__ void __launch_bounds__(256) snap_stats_merge_kernel(const SnapArgs a)
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)a.items * rows_all) return;
   const int64_t item = idx / rows_all, row = idx % rows_all;
+  if (a.redo && a.redo[item] == 0) return;
   float mx = -INFINITY;
   for (int s = 0; s < a.S; ++s) mx = fmaxf(mx, a.part_stats[(item * a.S + s) * rows_all + row].x);
   float l = 0.f;
@@ -463,6 +466,22 @@ __global__ void __launch_bounds__(256) snap_stats_merge_kernel(const SnapArgs a)
     l += p.y * fast_exp2(p.x - mx);
   }
   a.stats[idx] = make_float2(mx + log2f(l), 0.f);
+}
+
+// Row statistics supplied by the caller (the prefill's observation rows): copied into
+// a.stats; an item with a row marked y != 0 (a sum that lost precision) or a non-finite
+// one gets redo[item] = 1, so that pass 1 recomputes its rows from the keys.
+__global__ void __launch_bounds__(256) snap_stats_import_kernel(const SnapArgs a, const float2* given) {
+  const int rows_all = a.Hq * a.obs;
+  const int64_t item = blockIdx.x;
+  bool bad = false;
+  for (int row = threadIdx.x; row < rows_all; row += blockDim.x) {
+    const float2 v = given[item * rows_all + row];
+    a.stats[item * rows_all + row] = v;
+    bad |= v.y != 0.f || !__builtin_isfinite(v.x);
+  }
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) a.redo[item] = bad ? 1 : 0;
 }
 
 // out[item][n] = max(raw[n-1], raw[n], raw[n+1]) when n_blocks >= 3, else raw[n].
@@ -487,6 +506,7 @@ __global__ void __launch_bounds__(256) snap_scalar_stats_kernel(const SnapArgs a
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)a.items * rows_all) return;
   const int item = (int)(idx / rows_all), row = (int)(idx % rows_all);
+  if (a.redo && a.redo[item] == 0) return;
   const int h = row / a.obs, i = row % a.obs, g = h / a.n_rep;
   const uint16_t* qp = a.q + (int64_t)item * a.q_si + (int64_t)h * a.q_sh + (int64_t)i * a.q_st;
   float mx = -INFINITY, l = 0.f;
@@ -551,7 +571,7 @@ size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 struct SnapPlan {
   bool tiled;
   int hp, tw, parts, S, Kt, aligned, n_blocks, L_mid;
-  size_t part_off, stats_off, raw_off, total;
+  size_t part_off, stats_off, raw_off, redo_off, total;
 };
 
 SnapPlan snap_plan(int items, int seq_len, int sink, int obs, int num_q_heads, int n_rep, int head_dim,
@@ -591,10 +611,12 @@ SnapPlan snap_plan(int items, int seq_len, int sink, int obs, int num_q_heads, i
   p.part_off = 0;
   p.stats_off = a256((size_t)items * p.S * rows_all * sizeof(float2));
   p.raw_off = p.stats_off + a256((size_t)items * rows_all * sizeof(float2));
-  p.total = p.raw_off + a256((size_t)items * p.n_blocks * sizeof(float));
+  p.redo_off = p.raw_off + a256((size_t)items * p.n_blocks * sizeof(float));
+  p.total = p.redo_off + a256((size_t)items * sizeof(int32_t));
   return p;
 }
 
+// With a.redo set, pass 1 and the merge skip the items whose statistics were imported.
 template <int DT, int D, int TW>
 void launch_tiled(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
   const int64_t rows = (int64_t)a.items * a.Hq * a.obs;
@@ -615,7 +637,9 @@ void launch_tiled_tw(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
 }
 
 template <int DT>
-void launch_snap(const SnapArgs& a, const SnapPlan& p, hipStream_t st) {
+void launch_snap(const SnapArgs& a, const SnapPlan& p, hipStream_t st, const float2* given) {
+  if (given)
+    hipLaunchKernelGGL(snap_stats_import_kernel, dim3((unsigned)a.items), dim3(256), 0, st, a, given);
   if (p.tiled) {
     if (a.D == 64)
       launch_tiled_tw<DT, 64>(a, p, st);
@@ -665,12 +689,13 @@ extern "C" size_t ukv_snapkv_workspace_bytes(int layers, int seqs, int seq_len, 
   return snap_plan(layers * seqs, seq_len, sink_len, obs_len, num_q_heads, n_rep, head_dim, block_size, true).total;
 }
 
-extern "C" int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                                 const int32_t* block_table, int max_blocks, int num_pages, int layers, int seqs,
-                                 int seq_len, int sink_len, int obs_len, int num_q_heads, int num_kv_heads,
-                                 int head_dim, int n_rep, int block_size, float softmax_scale, int dtype,
-                                 float* scores, int64_t scores_stride, void* workspace, size_t workspace_bytes,
-                                 ukv_stream_t stream) {
+namespace {
+
+int snapkv_scores_impl(const void* q_obs, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                       const int32_t* block_table, int max_blocks, int num_pages, int layers, int seqs, int seq_len,
+                       int sink_len, int obs_len, int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                       int block_size, float softmax_scale, int dtype, const float* given_stats, float* scores,
+                       int64_t scores_stride, void* workspace, size_t workspace_bytes, ukv_stream_t stream) {
   if (!snap_shape_ok(layers, seqs, seq_len, sink_len, obs_len, num_q_heads, num_kv_heads, head_dim, n_rep,
                      block_size))
     return UKV_ERR_INVALID_ARGUMENT;
@@ -718,12 +743,42 @@ extern "C" int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, co
   a.part_stats = reinterpret_cast<float2*>(ws + p.part_off);
   a.stats = reinterpret_cast<float2*>(ws + p.stats_off);
   a.raw = reinterpret_cast<float*>(ws + p.raw_off);
+  a.redo = given_stats ? reinterpret_cast<int32_t*>(ws + p.redo_off) : nullptr;
   a.out = scores;
   a.out_stride = scores_stride;
+  const float2* given = reinterpret_cast<const float2*>(given_stats);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dtype == UKV_DTYPE_BF16)
-    launch_snap<UKV_DTYPE_BF16>(a, p, st);
+    launch_snap<UKV_DTYPE_BF16>(a, p, st, given);
   else
-    launch_snap<UKV_DTYPE_F16>(a, p, st);
+    launch_snap<UKV_DTYPE_F16>(a, p, st, given);
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int ukv_snapkv_scores(const void* q_obs, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                 const int32_t* block_table, int max_blocks, int num_pages, int layers, int seqs,
+                                 int seq_len, int sink_len, int obs_len, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int n_rep, int block_size, float softmax_scale, int dtype,
+                                 float* scores, int64_t scores_stride, void* workspace, size_t workspace_bytes,
+                                 ukv_stream_t stream) {
+  return snapkv_scores_impl(q_obs, q_strides, k, k_strides, block_table, max_blocks, num_pages, layers, seqs,
+                            seq_len, sink_len, obs_len, num_q_heads, num_kv_heads, head_dim, n_rep, block_size,
+                            softmax_scale, dtype, nullptr, scores, scores_stride, workspace, workspace_bytes,
+                            stream);
+}
+
+extern "C" int ukv_snapkv_scores_from_stats(const void* q_obs, const int64_t* q_strides, const void* k,
+                                            const int64_t* k_strides, const int32_t* block_table, int max_blocks,
+                                            int num_pages, int layers, int seqs, int seq_len, int sink_len,
+                                            int obs_len, int num_q_heads, int num_kv_heads, int head_dim, int n_rep,
+                                            int block_size, float softmax_scale, int dtype, const float* obs_stats,
+                                            float* scores, int64_t scores_stride, void* workspace,
+                                            size_t workspace_bytes, ukv_stream_t stream) {
+  if (!obs_stats || (reinterpret_cast<uintptr_t>(obs_stats) & 7u)) return UKV_ERR_INVALID_ARGUMENT;
+  return snapkv_scores_impl(q_obs, q_strides, k, k_strides, block_table, max_blocks, num_pages, layers, seqs,
+                            seq_len, sink_len, obs_len, num_q_heads, num_kv_heads, head_dim, n_rep, block_size,
+                            softmax_scale, dtype, obs_stats, scores, scores_stride, workspace, workspace_bytes,
+                            stream);
 }

@@ -15,6 +15,7 @@ from typing import Optional
 import torch
 
 from . import _ext
+from .snapkv import ObsStats
 
 _DTYPE_CODES = {torch.float16: _ext.UKV_DTYPE_F16, torch.bfloat16: _ext.UKV_DTYPE_BF16}
 
@@ -54,13 +55,24 @@ def write_chunk_kv(k_layer: torch.Tensor, v_layer: torch.Tensor, k_new: torch.Te
     _ext.check(code, "ukv_kv_write_varlen")
 
 
+def _host_ints(x):
+    return [int(v) for v in (x.tolist() if torch.is_tensor(x) else x)]
+
+
 def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                             block_table: torch.Tensor, cu_seqlens_q, kv_lens, *, softmax_scale: float, n_rep: int,
-                            max_chunk: Optional[int] = None) -> torch.Tensor:
+                            max_chunk: Optional[int] = None, obs_stats: Optional[ObsStats] = None,
+                            layer_id: Optional[int] = None, host_lens=None) -> torch.Tensor:
     """Causal attention of packed chunk queries q [total_q, H_q, D] over their sequences' pages.
 
     Query i of sequence b is at position kv_lens[b] - C_b + i and sees keys 0 .. that position.
     Returns [total_q, H_q, D] in q's dtype.
+
+    With ``obs_stats`` (and ``layer_id``), the chunk must be each sequence's last, holding at
+    least ``obs_stats.obs_len`` queries: layer ``layer_id``'s SnapKV normalisers of the last
+    ``obs_len`` queries are written alongside (ukv_paged_prefill_obs_stats). ``host_lens``:
+    (chunk lengths, sequence lengths) as host lists, saving the synchronisation that reading
+    device ``cu_seqlens_q`` / ``kv_lens`` back would cost.
     """
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4 or int(k_cache.shape[1]) != 16:
         raise RuntimeError("paged_prefill_shape_unsupported")
@@ -79,14 +91,42 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     B = int(lens.numel())
     if int(cu.numel()) != B + 1 or int(bt.shape[0]) != B:
         raise RuntimeError("paged_prefill_shape_unsupported:batch")
+    stats_view = None
+    if obs_stats is not None:
+        if layer_id is None:
+            raise ValueError("paged_prefill_attention: obs_stats needs layer_id")
+        if not isinstance(obs_stats, ObsStats):
+            raise TypeError("obs_stats must be an ObsStats")
+        if obs_stats.seqs != B or obs_stats.num_q_heads != Hq or obs_stats.data.device != dev:
+            raise RuntimeError("paged_prefill_shape_unsupported:obs_stats")
+        if not obs_stats.same_scale(softmax_scale):
+            raise RuntimeError("paged_prefill_shape_unsupported:obs_stats_scale")
+        # host copies of the chunk and sequence lengths (a sync when they are device tensors)
+        chunk_lens, seq_lens = host_lens if host_lens is not None else (None, None)
+        if chunk_lens is None:
+            cu_h = _host_ints(cu_seqlens_q)
+            chunk_lens = [cu_h[i + 1] - cu_h[i] for i in range(B)]
+            seq_lens = _host_ints(kv_lens)
+        if any(c < obs_stats.obs_len for c in chunk_lens):
+            raise RuntimeError("paged_prefill_shape_unsupported:obs_window_spans_chunks")
+        stats_view = obs_stats.layer_view(layer_id)
+    if dev.type != "cuda" or any(t.device != dev for t in (k_cache, v_cache, bt, cu, lens)):
+        raise RuntimeError("paged_prefill_unavailable:device")
     mc = _max_chunk(cu_seqlens_q, max_chunk)
     out = torch.empty((total_q, Hq, D), dtype=q.dtype, device=dev)
-    code = _ext.load().ukv_paged_prefill(
-        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), cu.data_ptr(), lens.data_ptr(),
-        out.data_ptr(), B, total_q, mc, Hq, Hkv, D, int(n_rep), int(bt.shape[1]),
-        min(int(k_cache.shape[0]), int(v_cache.shape[0])), _ext.i64_array(q.stride()[:2]),
-        _ext.i64_array(k_cache.stride()[:3]), _ext.i64_array(v_cache.stride()[:3]), float(softmax_scale),
-        _DTYPE_CODES[q.dtype], torch.cuda.current_stream(dev).cuda_stream)
+    args = [q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), cu.data_ptr(), lens.data_ptr(),
+            out.data_ptr(), B, total_q, mc, Hq, Hkv, D, int(n_rep), int(bt.shape[1]),
+            min(int(k_cache.shape[0]), int(v_cache.shape[0])), _ext.i64_array(q.stride()[:2]),
+            _ext.i64_array(k_cache.stride()[:3]), _ext.i64_array(v_cache.stride()[:3]), float(softmax_scale),
+            _DTYPE_CODES[q.dtype]]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if stats_view is None:
+        code = _ext.load().ukv_paged_prefill(*args, stream)
+    else:
+        code = _ext.load().ukv_paged_prefill_obs_stats(*args, obs_stats.sink_len, obs_stats.obs_len, *stats_view,
+                                                        stream)
+        if code == _ext.UKV_OK:
+            obs_stats.mark(layer_id, seq_lens)
     if code != _ext.UKV_OK:
         raise RuntimeError(f"paged_prefill_error:{_ext.status_string(code)}")
     return out
@@ -219,14 +259,21 @@ class PrefillPages:
         _ext.check(code, "ukv_kv_write_varlen")
 
     def attention(self, layer_id: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, *,
-                  softmax_scale: float, n_rep: int) -> torch.Tensor:
-        """Write the layer's chunk K/V, then causal attention of q [total_q, H_q, D] over prefix + chunk."""
+                  softmax_scale: float, n_rep: int, obs_stats: Optional[ObsStats] = None) -> torch.Tensor:
+        """Write the layer's chunk K/V, then causal attention of q [total_q, H_q, D] over prefix + chunk.
+
+        ``obs_stats``: this is the sequences' final chunk; also record layer ``layer_id``'s
+        SnapKV normalisers of the last ``obs_len`` queries (see ``snapkv.ObsStats``)."""
         c = self._open()
-        if c["total"] == 0:
+        if c["total"] == 0 and obs_stats is None:
             return torch.empty_like(q)
         self.write(layer_id, k_new, v_new)
+        host_lens = None
+        if obs_stats is not None:
+            host_lens = (c["lens"], [L + n for L, n in zip(self._lens, c["lens"])])
         return paged_prefill_attention(q, self.pool.k_cache[layer_id], self.pool.v_cache[layer_id], c["bt"], c["cu"],
-                                       c["kv"], softmax_scale=softmax_scale, n_rep=n_rep, max_chunk=c["max_chunk"])
+                                       c["kv"], softmax_scale=softmax_scale, n_rep=n_rep, max_chunk=c["max_chunk"],
+                                       obs_stats=obs_stats, layer_id=layer_id, host_lens=host_lens)
 
     def end_chunk(self) -> None:
         c = self._open()
