@@ -11,31 +11,35 @@
 // are read from 16-token pages through the block table, and
 // ukv_kv_write_varlen first writes the chunk's own K/V into its pages.
 //
-// Kernel: one workgroup of W waves (W = 8 by default, two per SIMD) takes
-// QW = W * 2 * (16 / n_rep) consecutive queries of one KV group. Within a
-// wave, an MFMA column is a (query, q head) pair: 16 / n_rep queries times the
-// n_rep q heads of the group, so one K/V read serves the whole GQA group; a
-// wave holds two 16-column blocks.
+// Kernel: one workgroup of W waves (W = 8, two per SIMD) takes QW = W * 3 *
+// (16 / n_rep) consecutive queries of one KV group. Within a wave, an MFMA
+// column is a (query, q head) pair: 16 / n_rep queries times the n_rep q heads
+// of the group, so one K/V read serves the whole GQA group; a wave holds three
+// 16-column blocks.
 //   * workgroups are ordered so that each XCD (dispatch is round-robin over the
 //     8 XCDs) runs consecutive work items: the query blocks of one (sequence,
 //     group) share that XCD's L2 while they stream the same pages;
-//   * key tiles of 32 keys (two pages) pass through registers into a 3-stage
-//     LDS ring (rows padded to 288 B), one barrier per tile; the loads of
-//     tiles t+2 and t+3 are in flight while tile t is computed;
+//   * key tiles of 32 keys (two pages) pass through registers into a 4-slot
+//     LDS ring (rows padded to 288 B), written two tiles ahead of their use,
+//     with a barrier after every second tile; the loads of tiles t+3 and t+4
+//     are in flight while tile t is computed;
 //   * S^T = K Q^T on v_mfma_f32_16x16x32 in the input type (A = 16 keys x 32
 //     dims from LDS, B = the wave's q columns in registers); lane l ends with
 //     keys 4*(l/16) + r of column l % 16;
 //   * online softmax per column in log2 units; masks only on tiles that touch
 //     the sequence end, an invalid page or the causal diagonal; the running max
-//     moves only when a score exceeds it by 2^8 (wave vote);
+//     moves only when a weight reaches 2^8 (wave vote on the packed weights);
 //   * P.V on v_mfma_f32_16x16x32_f16: P is rounded to fp16 (11 significant
 //     bits, 4x finer than a bf16 P) and, for bf16 pools, the loader converts
-//     the V tile to fp16, which is exact for |v| < 65520 (a tile holding a
-//     larger or infinite value stays bf16 and takes P as a bf16 value plus its
-//     bf16 residual on two MFMAs). The S^T layout is already P's A-operand
-//     layout; V's B operands come from 8 LDS row reads per lane regrouped
-//     with v_perm_b32; the softmax denominators come from one more MFMA
-//     against a ones operand, so they sum exactly the rounded P.
+//     the V tile to fp16, which is exact for |v| < 65520; a workgroup whose
+//     keys hold a larger or non-finite bf16 V recomputes its columns on an
+//     fp32 path. The S^T layout is already P's A-operand layout; V's B
+//     operands come from ds_read_b64_tr_b16 transpose reads; the softmax
+//     denominators come from one more MFMA against a ones operand, so they sum
+//     exactly the rounded P;
+//   * the STATS instance (the blocks holding each sequence's last obs queries,
+//     launched in the same grid) also sums the middle keys' fp32 weights into
+//     SnapKV's row statistics.
 #include <algorithm>
 #include <type_traits>
 #include <cmath>
@@ -64,7 +68,7 @@ struct PrefillArgs {
   // (.y = 0, or 1 where the sum lost precision), the row statistics the SnapKV scoring pass takes.
   float2* obs_stats;
   int64_t stats_seq_stride;
-  int sink, obs, n_obs_blocks, n_stats_wgs;
+  int sink, obs, n_obs_blocks;
 };
 
 __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
@@ -119,7 +123,7 @@ constexpr int kTileKeys = 32;
 #endif
 constexpr int kRowPad = UKV_PREFILL_KPAD;
 constexpr int kVRowPad = UKV_PREFILL_VPAD;
-constexpr int kStages = 3;
+constexpr int kStages = 4;  // K/V ring slots: tiles are written two ahead, a barrier every second tile
 constexpr int kColBlocks = 3;  // 16-column blocks per wave (3 measured 2.5 % faster than 2; 247 VGPRs)
 
 // Fallback for a workgroup whose key range holds a bf16 V value of magnitude
@@ -168,11 +172,12 @@ struct PrefillLds {
   __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kVRowPad];
 };
 
-// Workgroup wg of the tiled prefill. STATS: the workgroups of the query blocks that hold the
-// sequences' last obs queries (two column blocks per wave), which also produce those queries'
-// SnapKV row statistics.
+// Work item `item` of (sequence b, KV group g) of the tiled prefill. STATS: the blocks that
+// hold the sequence's last obs queries (two column blocks per wave), which also produce those
+// queries' SnapKV row statistics.
 template <int DT, int WAVES, bool STATS>
-__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg, PrefillLds& lds) {
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, const int g, const int item,
+                                             PrefillLds& lds) {
   constexpr int D = 128;
   constexpr int STEPS = D / 32;
   constexpr int NT = 64 * WAVES;
@@ -197,26 +202,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
   // query blocks from the one holding query C - obs.
   const int qw_main = WAVES * kColBlocks * qpb;
   auto obs_q0 = [&](int Cq) { return max(0, Cq - a.obs) / qw_main * qw_main; };
-  int q0, g, b;
-  if constexpr (STATS) {
-    const int j = wg % a.n_obs_blocks;
-    g = (wg / a.n_obs_blocks) % a.n_groups;
-    b = wg / (a.n_obs_blocks * a.n_groups);
-    if (b >= a.B) return;  // the count is rounded up to a multiple of 8
-    q0 = obs_q0(a.cu_q[b + 1] - a.cu_q[b]) + j * qw;
-  } else {
-    int qblk;
-    // Work item of this workgroup: each XCD takes a contiguous range.
-    const int n_qb = a.n_qblocks;
-    const int total = n_qb * a.n_groups * a.B;
-    const int xcd = wg & 7, slot = wg >> 3;
-    const int per = total >> 3, rem = total & 7;
-    const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
-    qblk = n_qb - 1 - work % n_qb;  // the longest query blocks of a group first
-    g = (work / n_qb) % a.n_groups;
-    b = work / (n_qb * a.n_groups);
-    q0 = qblk * qw;
-  }
+  // item: the STATS block of the (sequence, group) (from query obs_q0(C) on), or its main
+  // query block, the longest first
+  const int q0 = STATS ? obs_q0(a.cu_q[b + 1] - a.cu_q[b]) + item * qw : (a.n_qblocks - 1 - item) * qw;
   const int q_begin = a.cu_q[b];
   const int C = a.cu_q[b + 1] - q_begin;
   if (q0 >= C) return;  // whole workgroup
@@ -249,8 +237,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
   float m_ref[CB];  // running max of the column (log2 units)
   f32x4 o[CB][8];
   f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
-  // STATS: this lane's fp32 sum of 2^(s - m_ref) over its middle keys of column i16.
-  float lmid[STATS ? CB : 1];
+  // STATS: this lane's fp32 sum of 2^(s - m_ref) over its middle keys of column i16, and the
+  // current tile's share (added once the tile's max has settled).
+  float lmid[STATS ? CB : 1], tsum[STATS ? CB : 1];
   const int mid_end = STATS ? Lk - a.obs : 0;
   if constexpr (STATS)
 #pragma unroll
@@ -264,8 +253,8 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
   }
 
   // ---- tile loader: chunk idx = tid + i * NT is 16-byte chunk idx % 16 of key row idx / 16.
-  // Tile u is loaded into register set u & 1 three tiles ahead, written into
-  // ring slot u % 3 one tile ahead (zeroing rows past the sequence or on an
+  // Tile u is loaded into register set u & 1 four tiles ahead, written into
+  // ring slot u % 4 two tiles ahead (zeroing rows past the sequence or on an
   // invalid page and converting a bf16 V to fp16), and computed at tile u.
   // The block table is read through the constant address space: the kernel
   // never writes it, and this keeps the wave-uniform page-id loads on the
@@ -329,15 +318,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
     t_id[j][0] = page_id(2 * j);
     t_id[j][1] = page_id(2 * j + 1);
   }
-  // Prologue: tile 0 into the ring, tiles 1 and 2 in flight. Loads are issued
+  // Prologue: tiles 0 and 1 into the ring, tiles 2 and 3 in flight. Loads are issued
   // unconditionally (tiles past the end read page 0 and are never used) so
   // that every wait is on loads of a fixed age: vmcnt(2) on the older set.
   issue(t_id[0][0], t_id[0][1], rk0, rv0);
   issue(t_id[1][0], t_id[1][1], rk1, rv1);
   store(0, 0, t_id[0][0], t_id[0][1], rk0, rv0);
   issue(t_id[2][0], t_id[2][1], rk0, rv0);
+  store(1, 1, t_id[1][0], t_id[1][1], rk1, rv1);
+  issue(t_id[3][0], t_id[3][1], rk1, rv1);
   int id_n0 = page_id(8), id_n1 = page_id(9);  // page ids of tile t+4
-  // Retire every load issued so far (q columns, tiles 1 and 2) once, so that
+  // Retire every load issued so far (q columns, tiles 2 and 3) once, so that
   // no wait for them is left inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
@@ -392,15 +383,24 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
       pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                      pack_f16(p[1][2], p[1][3])};
       if constexpr (STATS) {
-        if (!mid_none) {
+        // (mid_all and mid_none are wave-uniform: only the tiles straddling a boundary mask)
+        float ts = 0.f;
+        if (mid_all) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ts += p[kb][r];
+        } else if (!mid_none) {
+          const int lo = a.sink - key0 - 4 * kg, hi = mid_end - key0 - 4 * kg;  // this lane's middle offsets
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int key = key0 + kb * 16 + 4 * kg + r;
-              lmid[cb] += (mid_all || (key >= a.sink && key < mid_end)) ? p[kb][r] : 0.f;
+              const int d = kb * 16 + r;
+              ts += ((d >= lo) & (d < hi)) ? p[kb][r] : 0.f;
             }
         }
+        tsum[cb] = ts;
       }
     };
     // Moves column block cb's max to the tile's where that lies more than kTau above it,
@@ -427,27 +427,28 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
       if constexpr (STATS) lmid[cb] *= alpha;  // lane-local: column i16, like m_ref
       return true;
     };
-    if constexpr (STATS) {
-      // The middle sums take every weight once, in fp32: settle the max before the weights.
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        settle(cb);
-        exp_pack(cb);
-      }
-    } else {
+    {
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) exp_pack(cb);
-      u16x2 pmax = as_u16x2(pa[0][0]);
+      // The max of the packed weights with three-input fp16 maxima (v_pk_maximum3_f16): a NaN
+      // weight makes the maximum NaN, whose pattern, like inf's, lies above the threshold.
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      auto hv = [&](int i) { return __builtin_bit_cast(h2, pa[i / 4][i % 4]); };
+      h2 mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hv(0), hv(1)), hv(2));
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) pmax = __builtin_elementwise_max(pmax, as_u16x2(pa[cb][c]));
+      for (int i = 3; i + 1 < 4 * CB; i += 2)
+        mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx, hv(i)), hv(i + 1));
+      if constexpr ((4 * CB - 3) % 2) mx = __builtin_elementwise_maximum(mx, hv(4 * CB - 1));
+      const u16x2 pmax = __builtin_bit_cast(u16x2, mx);
       if (__any(__builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(pmax, u16x2{0x5BFF, 0x5BFF})) != 0u)) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
           if (settle(cb)) exp_pack(cb);
       }
     }
+    if constexpr (STATS)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) lmid[cb] += tsum[cb];
     // P.V: the B operand of output tile e (dims 16e .. 16e + 15) holds, in lane
     // (i16, kg), dim 16e + i16 of keys 4kg..4kg+3 and 16+4kg..16+4kg+3 (the
     // key order of P's A operand). ds_read_b64_tr_b16 builds it from row-major
@@ -468,17 +469,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
       lacc[cb] = mfma16x16x32<UKV_DTYPE_F16>(pa[cb], u32x4{ones_f16, ones_f16, ones_f16, ones_f16}, lacc[cb]);
   };
 
-  // Tile t: (a) tile t+1 from register set (t+1)&1 into ring slot (t+1)%3;
-  // (b) tile t+3 into that register set; (c) tile t on this wave's columns;
-  // (d) barrier: slot (t+1)%3 becomes visible.
+  // Tile t: (a) tile t+2 from register set t&1 into ring slot (t+2)%4; (b) tile t+4 into that
+  // set; (c) tile t on this wave's columns; (d) after an odd t, a barrier. A slot written at
+  // step t is read at step t+2 and written again at step t+4: a barrier after every odd step
+  // lies between each write and its reads, and between each read and the next write.
   auto step = [&](int t, int slot, auto set_parity, auto do_compute) {
-    constexpr int P1 = decltype(set_parity)::value;  // parity of tile t+1
-    int nslot = slot + 1 == kStages ? 0 : slot + 1;
+    constexpr int P = decltype(set_parity)::value;  // parity of t
+    const int wslot = (slot + 2) & 3;
     // (a slot written past the last tile is never read)
-    if constexpr (P1 == 0) store(t + 1, nslot, t_id[1][0], t_id[1][1], rk0, rv0);
-    else store(t + 1, nslot, t_id[1][0], t_id[1][1], rk1, rv1);
-    if constexpr (P1 == 0) issue(t_id[3][0], t_id[3][1], rk0, rv0);
-    else issue(t_id[3][0], t_id[3][1], rk1, rv1);
+    if constexpr (P == 0) store(t + 2, wslot, t_id[2][0], t_id[2][1], rk0, rv0);
+    else store(t + 2, wslot, t_id[2][0], t_id[2][1], rk1, rv1);
+    if constexpr (P == 0) issue(id_n0, id_n1, rk0, rv0);
+    else issue(id_n0, id_n1, rk1, rv1);
     do_compute(t, slot);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
@@ -489,16 +491,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
     t_id[3][1] = id_n1;
     id_n0 = page_id(2 * (t + 5));
     id_n1 = page_id(2 * (t + 5) + 1);
-    __syncthreads();
-    return nslot;
+    if constexpr (P == 1) __syncthreads();
+    return (slot + 1) & 3;
   };
   using Even = std::integral_constant<int, 0>;
   using Odd = std::integral_constant<int, 1>;
   auto run = [&](auto do_compute) {
     int slot = 0;
     for (int t = 0; t < n_tiles; t += 2) {
-      slot = step(t, slot, Odd{}, do_compute);  // tile t+1 is odd
-      if (t + 1 < n_tiles) slot = step(t + 1, slot, Even{}, do_compute);
+      slot = step(t, slot, Even{}, do_compute);
+      if (t + 1 < n_tiles) slot = step(t + 1, slot, Odd{}, do_compute);
     }
   };
   if (wave_live) run(compute);
@@ -564,23 +566,27 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int wg,
   }
 }
 
-// One launch: with WITH_STATS, workgroups 0 .. n_stats_wgs - 1 (a multiple of 8, so that
-// workgroup wg of the rest still runs on XCD wg % 8) are the STATS blocks - the longest of
-// every (sequence, group), dispatched first - and the rest the other query blocks.
+// Work items: for each (sequence, KV group), n_obs_blocks STATS blocks (WITH_STATS only;
+// they hold the longest queries) and then n_qblocks main query blocks, the longest first.
+// Each XCD (dispatch is round-robin over the 8 XCDs) takes a contiguous range of items, so
+// that the blocks of one (sequence, group) share that XCD's L2 while they stream its pages.
 template <int DT, int WAVES, bool WITH_STATS>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 paged_prefill_kernel(const PrefillArgs a) {
   __shared__ PrefillLds lds;
-  if constexpr (WITH_STATS) {
-    const int ns = a.n_stats_wgs;
-    if ((int)blockIdx.x < ns) {
-      prefill_tile<DT, WAVES, true>(a, blockIdx.x, lds);
-      return;
-    }
-    prefill_tile<DT, WAVES, false>(a, blockIdx.x - ns, lds);
-  } else {
-    prefill_tile<DT, WAVES, false>(a, blockIdx.x, lds);
-  }
+  const int n_s = WITH_STATS ? a.n_obs_blocks : 0;
+  const int n_items = n_s + a.n_qblocks;
+  const int total = n_items * a.n_groups * a.B;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int per = total >> 3, rem = total & 7;
+  const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
+  const int item = work % n_items;
+  const int pair = work / n_items;
+  const int g = pair % a.n_groups, b = pair / a.n_groups;
+  if (WITH_STATS && item < n_s)
+    prefill_tile<DT, WAVES, true>(a, b, g, item, lds);
+  else
+    prefill_tile<DT, WAVES, false>(a, b, g, item - n_s, lds);
 }
 
 // Reference-order scalar prefill for shapes the MFMA kernel does not cover: one
@@ -878,9 +884,8 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
       // than obs + qw of them.
       const int qw_stats = W * 2 * (16 / n_rep);
       a.n_obs_blocks = (a.obs + qw - 1 + qw_stats - 1) / qw_stats;
-      const int64_t swgs = ((int64_t)a.n_obs_blocks * n_groups * batch + 7) / 8 * 8;
+      const int64_t swgs = (int64_t)a.n_obs_blocks * n_groups * batch;
       if (swgs + wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
-      a.n_stats_wgs = (int)swgs;
       const dim3 grid((unsigned)(swgs + wgs));
       if (dtype == UKV_DTYPE_BF16)
         hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), grid, dim3(64 * W), 0, stream, a);
