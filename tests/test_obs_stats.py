@@ -282,3 +282,26 @@ def test_a_dominant_sink_flags_the_rows_and_the_scores_stay_exact(cuda):
     one = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
     two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
     assert np.array_equal(one, two)
+
+
+@pytest.mark.gpu
+def test_scores_from_prefill_rows_on_the_scalar_scoring_path(cuda):
+    # obs_len 40 is not a multiple of 16: the scores run the scalar kernel pair, which takes the
+    # imported rows the same way (and recomputes a flagged item's rows from the keys)
+    sink, obs, layers = 5, 40, 2
+    r = _prefill(cuda, "bf16", [[300, 300], [200, 200]], Hq=8, Hkv=2, layers=layers, sink=sink, obs=obs, seed=21)
+    r["q_dev"] = _dev(r["q_obs"], "bf16")
+    one = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
+    np.testing.assert_allclose(one, two, rtol=1e-5, atol=1e-8)   # both sides sum fp32 weights here
+    for b in range(2):
+        for layer in range(layers):
+            want = so.score_layer_blocks(_f(r["dense"][layer][b], "bf16"), _f(r["q_obs"][b, layer], "bf16"),
+                                         sink_len=sink, obs_len=obs, n_rep=r["n_rep"])
+            err = np.abs(one[b * layers + layer] - want)
+            assert np.all(err <= 1e-4 * np.abs(want).max() + 1e-3 * np.abs(want)), (b, layer, err.max())
+    r["st"].data[0, 1, 2, 7, 1] = 1.0                          # flag one row of item (seq 0, layer 1)
+    r["st"].data[0, 1, 2, 7, 0] = -1e30
+    got = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    for item in range(2 * layers):
+        assert np.array_equal(got[item], two[item] if item == 1 else one[item]), item
