@@ -849,8 +849,8 @@ def run_compacted_decode(args, dev):
 
 def prefill_stats_leg(pool, table, lists, dev, seed, steps):
     """The statistics path: the sequences' final prefill chunk (their last 2048 tokens, keys
-    already in the pool) run for all 32 layers with and without ObsStats (interleaved rounds,
-    HIP events around each 32-layer pass), then score_blocks from those statistics. Returns
+    already in the pool) run for all 32 layers with and without ObsStats (each layer's two calls
+    back to back, HIP events around each call), then score_blocks from those statistics. Returns
     (extra prefill ms per 32 layers, plain prefill ms, score ms, score per-call ms, scores,
     two-pass scores of the same queries)."""
     import torch
@@ -870,30 +870,37 @@ def prefill_stats_leg(pool, table, lists, dev, seed, steps):
     q_obs = qc.view(B, C, Hq, D)[:, C - obs:].permute(0, 2, 1, 3).unsqueeze(1).expand(B, L, Hq, obs, D).contiguous()
     host_lens = ([C] * B, [ctx] * B)
 
-    def pass_plain():
-        for layer in range(L):
-            prefill.paged_prefill_attention(qc, pool.k_cache[layer], pool.v_cache[layer], table, cu, lens,
-                                            softmax_scale=scale, n_rep=Hq // Hkv, max_chunk=C)
+    def one_layer(layer, stats):
+        kw = dict(obs_stats=st, layer_id=layer, host_lens=host_lens) if stats else {}
+        prefill.paged_prefill_attention(qc, pool.k_cache[layer], pool.v_cache[layer], table, cu, lens,
+                                        softmax_scale=scale, n_rep=Hq // Hkv, max_chunk=C, **kw)
 
-    def pass_stats():
-        for layer in range(L):
-            prefill.paged_prefill_attention(qc, pool.k_cache[layer], pool.v_cache[layer], table, cu, lens,
-                                            softmax_scale=scale, n_rep=Hq // Hkv, max_chunk=C, obs_stats=st,
-                                            layer_id=layer, host_lens=host_lens)
-
-    pass_plain()
-    pass_stats()
+    for layer in range(L):  # warm-up; every layer's rows written
+        one_layer(layer, True)
+    one_layer(0, False)
     torch.cuda.synchronize()
-    t_plain, t_stats = [], []
-    for _ in range(2):
-        for fn, acc in ((pass_plain, t_plain), (pass_stats, t_stats)):
-            a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn()
-            z.record()
-            torch.cuda.synchronize()
-            acc.append(a.elapsed_time(z))
-    plain_ms, stats_ms = min(t_plain), min(t_stats)
+    # Each layer's call with and without the statistics back to back, in alternating order, so
+    # that clock drift over the run cancels from the difference; 3 rounds over the 32 layers.
+    rounds = 3
+    diff_ms, plain_ms = 0.0, 0.0
+    for r in range(rounds):
+        evs = []
+        for layer in range(L):
+            order = (False, True) if (r + layer) % 2 == 0 else (True, False)
+            pair = {}
+            for stats in order:
+                a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                one_layer(layer, stats)
+                z.record()
+                pair[stats] = (a, z)
+            evs.append(pair)
+        torch.cuda.synchronize()
+        for pair in evs:
+            t_plain, t_stats = (pair[k][0].elapsed_time(pair[k][1]) for k in (False, True))
+            diff_ms += (t_stats - t_plain) / rounds
+            plain_ms += t_plain / rounds
+    stats_ms = plain_ms + diff_ms
 
     def score():
         return snapkv.score_blocks(q_obs, pool.k_cache, table, seq_len=ctx, sink_len=sink, obs_len=obs,
