@@ -282,9 +282,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       // rows 0-15 of a tile come from its first page, rows 16-31 from the second
       const int second = __builtin_amdgcn_readfirstlane((tid + i * NT) >> 8);
       const int id = second ? id1 : id0;
-      const int64_t pg = page_ok(id) ? id : 0;
-      gload16(rk[i], a.k + pg * a.k_sp + koff[i]);
-      gload16(rv[i], a.v + pg * a.v_sp + voff[i]);
+      // page strides fit 32 bits (checked on the host): a 32 x 32 -> 64-bit scalar product
+      const uint32_t pg = page_ok(id) ? (uint32_t)id : 0u;
+      gload16(rk[i], a.k + (uint64_t)pg * (uint32_t)a.k_sp + koff[i]);
+      gload16(rv[i], a.v + (uint64_t)pg * (uint32_t)a.v_sp + voff[i]);
     }
   };
   bool wide_mine = false;  // this thread saw a bf16 V value fp16 cannot hold
@@ -472,16 +473,18 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   // Tile t: (a) tile t+2 from register set t&1 into ring slot (t+2)%4; (b) tile t+4 into that
   // set; (c) tile t on this wave's columns; (d) after an odd t, a barrier. A slot written at
   // step t is read at step t+2 and written again at step t+4: a barrier after every odd step
-  // lies between each write and its reads, and between each read and the next write.
-  auto step = [&](int t, int slot, auto set_parity, auto do_compute) {
-    constexpr int P = decltype(set_parity)::value;  // parity of t
-    const int wslot = (slot + 2) & 3;
+  // lies between each write and its reads, and between each read and the next write. The loop
+  // is unrolled by the ring's four slots, so slots and register sets are compile-time constants
+  // (LDS offsets fold into the instructions; register sets never meet at a runtime join).
+  auto step = [&](int t, auto phase, auto do_compute) {
+    constexpr int Q = decltype(phase)::value;  // t % 4: the ring slot of tile t
+    constexpr int P = Q & 1;                   // register set of tile t+2
     // (a slot written past the last tile is never read)
-    if constexpr (P == 0) store(t + 2, wslot, t_id[2][0], t_id[2][1], rk0, rv0);
-    else store(t + 2, wslot, t_id[2][0], t_id[2][1], rk1, rv1);
+    if constexpr (P == 0) store(t + 2, (Q + 2) & 3, t_id[2][0], t_id[2][1], rk0, rv0);
+    else store(t + 2, (Q + 2) & 3, t_id[2][0], t_id[2][1], rk1, rv1);
     if constexpr (P == 0) issue(id_n0, id_n1, rk0, rv0);
     else issue(id_n0, id_n1, rk1, rv1);
-    do_compute(t, slot);
+    do_compute(t, Q);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       t_id[j][0] = t_id[j + 1][0];
@@ -492,15 +495,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
     id_n0 = page_id(2 * (t + 5));
     id_n1 = page_id(2 * (t + 5) + 1);
     if constexpr (P == 1) __syncthreads();
-    return (slot + 1) & 3;
   };
-  using Even = std::integral_constant<int, 0>;
-  using Odd = std::integral_constant<int, 1>;
   auto run = [&](auto do_compute) {
-    int slot = 0;
-    for (int t = 0; t < n_tiles; t += 2) {
-      slot = step(t, slot, Even{}, do_compute);
-      if (t + 1 < n_tiles) slot = step(t + 1, slot, Odd{}, do_compute);
+    for (int t = 0; t < n_tiles; t += 4) {
+      step(t, std::integral_constant<int, 0>{}, do_compute);
+      if (t + 1 < n_tiles) step(t + 1, std::integral_constant<int, 1>{}, do_compute);
+      if (t + 2 < n_tiles) step(t + 2, std::integral_constant<int, 2>{}, do_compute);
+      if (t + 3 < n_tiles) step(t + 3, std::integral_constant<int, 3>{}, do_compute);
     }
   };
   if (wave_live) run(compute);
@@ -855,9 +856,10 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
   auto in_page_ok = [&](int64_t st, int64_t sh) {
     return st >= 0 && sh >= 0 && 15 * st + (int64_t)(num_kv_heads - 1) * sh + head_dim <= (int64_t)UINT32_MAX;
   };
+  auto page_stride_ok = [](int64_t sp) { return sp >= 0 && sp <= (int64_t)UINT32_MAX; };
   const bool strides_ok = mul8(a.q_st) && mul8(a.q_sh) && mul8(a.k_sp) && mul8(a.k_st) && mul8(a.k_sh) &&
                           mul8(a.v_sp) && mul8(a.v_st) && mul8(a.v_sh) && in_page_ok(a.k_st, a.k_sh) &&
-                          in_page_ok(a.v_st, a.v_sh);
+                          in_page_ok(a.v_st, a.v_sh) && page_stride_ok(a.k_sp) && page_stride_ok(a.v_sp);
   const bool fast = head_dim == 128 && softmax_scale > 0.f && std::isfinite(softmax_scale) && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
                     strides_ok && al16(q) && al16(out) && al16(k_cache) && al16(v_cache) && max_blocks > 0;
   if (obs) {
