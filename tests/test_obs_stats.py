@@ -305,3 +305,31 @@ def test_scores_from_prefill_rows_on_the_scalar_scoring_path(cuda):
     got = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
     for item in range(2 * layers):
         assert np.array_equal(got[item], two[item] if item == 1 else one[item]), item
+
+
+def test_c_entry_points_refuse_bad_statistics_arguments_before_any_launch():
+    # every refusal below returns before the library touches a device
+    from unifiedkv_amd import _ext
+
+    lib = _ext.load()
+    i64 = _ext.i64_array
+    q_st, kv_st = i64((32 * 128, 128)), i64((16 * 8 * 128, 8 * 128, 128))
+
+    def prefill_stats(sink, obs, stats, stride):
+        return lib.ukv_paged_prefill_obs_stats(None, None, None, None, None, None, None, 2, 64, 32, 32, 8, 128, 4,
+                                               4, 16, q_st, kv_st, kv_st, 0.088, _ext.UKV_DTYPE_BF16, sink, obs,
+                                               stats, stride, None)
+
+    assert prefill_stats(4, 16, None, 32 * 16) == _ext.UKV_ERR_INVALID_ARGUMENT        # no buffer
+    assert prefill_stats(4, 16, 0x1004, 32 * 16) == _ext.UKV_ERR_INVALID_ARGUMENT      # not 8-byte aligned
+    assert prefill_stats(4, 16, 0x1000, 32 * 16 - 1) == _ext.UKV_ERR_INVALID_ARGUMENT  # rows overlap
+    assert prefill_stats(-1, 16, 0x1000, 32 * 16) == _ext.UKV_ERR_INVALID_ARGUMENT     # negative sink
+    assert prefill_stats(4, 0, 0x1000, 32 * 16) == _ext.UKV_ERR_INVALID_ARGUMENT       # empty window
+
+    def scores_from(stats):
+        return lib.ukv_snapkv_scores_from_stats(None, i64((0, 0, 0)), None, i64((0, 0, 0, 0)), None, 0, 0, 1, 1,
+                                                4096, 64, 128, 32, 8, 128, 4, 16, 0.088, _ext.UKV_DTYPE_BF16, stats,
+                                                None, 0, None, 0, None)
+
+    assert scores_from(None) == _ext.UKV_ERR_INVALID_ARGUMENT
+    assert scores_from(0x1004) == _ext.UKV_ERR_INVALID_ARGUMENT
