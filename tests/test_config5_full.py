@@ -10,6 +10,8 @@
 (c) decode at B=8, L=6704 on the compacted tables: two sampled sequences of two layers against
     the fp64 oracle (|gpu - oracle| <= 2e-3 + 1e-2 |oracle|), and bit-identical output after a
     random relabelling of every physical page.
+(0) first, on the uncompacted pool: the SnapKV scores from the row statistics of the sequences'
+    final prefill chunk against the two-pass scores and fp64 row sums.
 """
 import gc
 
@@ -75,6 +77,60 @@ def c5(cuda):
 def _src_ids(lists, ret):
     """Physical source ids per sequence: [layers, keep] from the oracle's retained logical pages."""
     return [np.asarray(pages)[r] for pages, r in zip(lists, ret)]
+
+
+def test_0_scores_from_final_chunk_statistics_full_size(c5, cuda):
+    """(0) SnapKV scores with the row statistics of each sequence's final 2048-token chunk (layers 0
+    and 31 through a strided two-layer view of the pool): equal to the two-pass scores within the
+    two-pass path's own fp16 rounding, and sampled rows within 5e-6 (log2 units) of fp64 sums."""
+    import math
+
+    from oracle import snapkv_oracle as so
+    from unifiedkv_amd import prefill, snapkv
+    from unifiedkv_amd.pool import pack_block_table
+
+    pool, lists = c5["pool"], c5["lists"]
+    C, scale, n_rep = 2048, D ** -0.5, HQ // HKV
+    layers = (0, LAYERS - 1)
+    table = torch.from_numpy(pack_block_table(lists)).to(cuda)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(SEED + 3)
+    qc = torch.randn((SEQS * C, HQ, D), generator=g, device=cuda).to(torch.bfloat16)
+    cu = torch.arange(0, SEQS * C + 1, C, dtype=torch.int32, device=cuda)
+    lens = torch.full((SEQS,), CTX, dtype=torch.int32, device=cuda)
+    st = snapkv.ObsStats(SEQS, len(layers), HQ, sink_len=SINK, obs_len=OBS, softmax_scale=scale, device=cuda)
+    for j, layer in enumerate(layers):
+        prefill.paged_prefill_attention(qc, pool.k_cache[layer], pool.v_cache[layer], table, cu, lens,
+                                        softmax_scale=scale, n_rep=n_rep, max_chunk=C, obs_stats=st, layer_id=j,
+                                        host_lens=([C] * SEQS, [CTX] * SEQS))
+    q_obs = qc.view(SEQS, C, HQ, D)[:, C - OBS:].permute(0, 2, 1, 3).unsqueeze(1)
+    q_obs = q_obs.expand(SEQS, len(layers), HQ, OBS, D).contiguous()
+    kview = pool.k_cache[0::LAYERS - 1]                      # layers 0 and 31, no copy
+    assert kview.shape[0] == 2 and kview.data_ptr() == pool.k_cache[0].data_ptr()
+    one = snapkv.score_blocks(q_obs, kview, table, seq_len=CTX, sink_len=SINK, obs_len=OBS, n_rep=n_rep,
+                              obs_stats=st).cpu().numpy()
+    two = snapkv.score_blocks(q_obs, kview, table, seq_len=CTX, sink_len=SINK, obs_len=OBS,
+                              n_rep=n_rep).cpu().numpy()
+    rel = np.abs(one - two) / np.maximum(np.abs(two), 1e-30)
+    log(f"scores from statistics against two passes: max rel diff {rel.max():.2e}")
+    assert np.all(np.abs(one - two) <= 2.0 ** -9 * np.abs(two) + 1e-7)
+    data = st.data.cpu().numpy()
+    assert np.all(data[..., 1] == 0)
+    rng = np.random.default_rng(SEED + 13)
+    worst = 0.0
+    for b in sorted(rng.choice(SEQS, 2, replace=False)):
+        for j, layer in enumerate(layers):
+            ids = torch.tensor(lists[b], dtype=torch.long, device=cuda)
+            for h in sorted(rng.choice(HQ, 2, replace=False)):
+                kg = pool.k_cache[layer, ids][:, :, h // n_rep].reshape(-1, D).float().cpu().numpy()
+                rows = sorted(rng.choice(OBS, 3, replace=False))
+                qr = q_obs[b, j, h, rows].float().cpu().numpy()
+                want = so.obs_row_stats(kg[None], qr[None], sink_len=SINK, obs_len=OBS, n_rep=1, scale=scale)[0]
+                err = np.abs(data[b, j, h, rows, 0] - want).max()
+                worst = max(worst, err)
+                assert err <= 5e-6, (b, layer, h, err)
+    log(f"final-chunk row statistics within {worst:.2e} of fp64 (log2 units)")
+    assert math.isfinite(worst)
 
 
 def test_a_compaction_full_size(c5, cuda):
