@@ -428,7 +428,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       if constexpr (STATS) lmid[cb] *= alpha;  // lane-local: column i16, like m_ref
       return true;
     };
-    {
+    {  // the tile's weights, then the vote on them
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) exp_pack(cb);
       // The max of the packed weights with three-input fp16 maxima (v_pk_maximum3_f16): a NaN
