@@ -328,8 +328,9 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  * stats_seq_stride counts (value, flag) pairs and is at least num_q_heads * obs_len; obs_stats is
  * 8-byte aligned. For the layout ukv_snapkv_scores_from_stats reads ([seqs][layers][num_q_heads]
  * [obs_len] pairs) pass obs_stats + 2 * layer * num_q_heads * obs_len and stats_seq_stride =
- * layers * num_q_heads * obs_len. Needs the tiled path (head_dim 128, n_rep 1/2/4/8/16, 16-byte
- * aligned rows: UKV_ERR_INVALID_ARGUMENT otherwise) and C_b >= obs_len for the rows to exist.
+ * layers * num_q_heads * obs_len. The rows come from the tiled kernel (head_dim 128, n_rep
+ * 1/2/4/8/16, 16-byte aligned rows); on the scalar path every row is written flagged (0, 1), so the
+ * scores recompute them. C_b >= obs_len for the rows to exist.
  * The reference captures the window's queries in its q_proj hook (core/scheduler.py:269-341)
  * and normalises their softmax over K_mid at selection time (core/scheduler.py:565-592,
  * core/compress.py:116-130); here that normaliser is taken while the prefill streams the keys.

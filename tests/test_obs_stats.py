@@ -333,3 +333,41 @@ def test_c_entry_points_refuse_bad_statistics_arguments_before_any_launch():
 
     assert scores_from(None) == _ext.UKV_ERR_INVALID_ARGUMENT
     assert scores_from(0x1004) == _ext.UKV_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.gpu
+def test_shapes_off_the_tiled_prefill_flag_every_row(cuda):
+    # head_dim 64 runs the scalar prefill: it writes every row flagged, and the scores then equal
+    # the two-pass scores bit for bit (every item recomputed)
+    import torch
+
+    from unifiedkv_amd import snapkv
+    from unifiedkv_amd.pool import PagedKVPool
+    from unifiedkv_amd.prefill import PrefillPages
+
+    rng = np.random.default_rng(31)
+    B, L, Hq, Hkv, D, sink, obs, C = 2, 2, 8, 2, 64, 4, 32, 300
+    scale = D ** -0.5
+    pool = PagedKVPool(16, L, Hkv, D, torch.bfloat16, num_blocks=64, device=cuda)
+    pp = PrefillPages(pool, B)
+    st = snapkv.ObsStats(B, L, Hq, sink_len=sink, obs_len=obs, softmax_scale=scale, device=cuda)
+    st.data.fill_(7.0)
+    pp.begin_chunk([C] * B)
+    q_obs = np.zeros((B, L, Hq, obs, D), np.uint16)
+    for layer in range(L):
+        q, k, v = _bits(rng, (B * C, Hq, D), "bf16"), _bits(rng, (B * C, Hkv, D), "bf16"), _bits(rng, (B * C, Hkv, D), "bf16")
+        pp.attention(layer, _dev(q, "bf16"), _dev(k, "bf16"), _dev(v, "bf16"), softmax_scale=scale, n_rep=Hq // Hkv,
+                     obs_stats=st)
+        for b in range(B):
+            q_obs[b, layer] = q[(b + 1) * C - obs:(b + 1) * C].transpose(1, 0, 2)
+    pp.end_chunk()
+    data = st.data.cpu().numpy()
+    assert np.all(data[..., 1] == 1.0) and np.all(data[..., 0] == 0.0)
+    width = max(len(x) for x in pp.page_lists)
+    table = torch.tensor([x + [0] * (width - len(x)) for x in pp.page_lists], dtype=torch.int32, device=cuda)
+    qd = _dev(q_obs, "bf16")
+    one = snapkv.score_blocks(qd, pool.k_cache, table, seq_len=C, sink_len=sink, obs_len=obs, n_rep=Hq // Hkv,
+                              obs_stats=st).cpu().numpy()
+    two = snapkv.score_blocks(qd, pool.k_cache, table, seq_len=C, sink_len=sink, obs_len=obs,
+                              n_rep=Hq // Hkv).cpu().numpy()
+    assert np.array_equal(one, two)

@@ -590,6 +590,15 @@ paged_prefill_kernel(const PrefillArgs a) {
     prefill_tile<DT, WAVES, false>(a, b, g, item - n_s, lds);
 }
 
+// Marks every observation row of the call as recomputed-by-the-scorer: (0, 1) at row
+// obs_stats[b * stats_seq_stride + h * obs + i] for b < B, h < Hq, i < obs.
+__global__ void __launch_bounds__(256) obs_flag_kernel(const PrefillArgs a, const int64_t rows) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows) return;
+  const int64_t per = (int64_t)a.Hq * a.obs;
+  a.obs_stats[(idx / per) * a.stats_seq_stride + idx % per] = make_float2(0.f, 1.f);
+}
+
 // Reference-order scalar prefill for shapes the MFMA kernel does not cover: one
 // workgroup per (q head, query row); natural exp; keys 0 .. P + i in page order.
 template <int DT>
@@ -863,7 +872,6 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
   const bool fast = head_dim == 128 && softmax_scale > 0.f && std::isfinite(softmax_scale) && (n_rep == 1 || n_rep == 2 || n_rep == 4 || n_rep == 8 || n_rep == 16) &&
                     strides_ok && al16(q) && al16(out) && al16(k_cache) && al16(v_cache) && max_blocks > 0;
   if (obs) {
-    if (!fast) return UKV_ERR_INVALID_ARGUMENT;  // the statistics come from the tiled kernel only
     a.obs_stats = static_cast<float2*>(obs->stats);
     a.stats_seq_stride = obs->seq_stride;
     a.sink = obs->sink;
@@ -900,6 +908,13 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
       hipLaunchKernelGGL(paged_prefill_scalar_kernel<UKV_DTYPE_BF16>, grid, dim3(256), 0, stream, a);
     else
       hipLaunchKernelGGL(paged_prefill_scalar_kernel<UKV_DTYPE_F16>, grid, dim3(256), 0, stream, a);
+    // The statistics come from the tiled kernel only: here every row is flagged, and the
+    // scoring pass recomputes them from the keys.
+    if (obs) {
+      const int64_t rows = (int64_t)batch * num_q_heads * a.obs;
+      if (rows > 0)
+        hipLaunchKernelGGL(obs_flag_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, a, rows);
+    }
   }
   return hipGetLastError() == hipSuccess ? UKV_OK : UKV_ERR_LAUNCH;
 }
