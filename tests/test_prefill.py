@@ -16,6 +16,7 @@ from oracle import oracle, prefill_oracle
 from unifiedkv_amd import workloads
 
 ATOL, RTOL = 2e-3, 1e-2
+LSE_TOL_JUMP = 5e-6  # log2 units, on top of the fp32 dot-product bound
 
 
 def make_case(seed, prefix, chunk, Hq=32, Hkv=8, D=128, dtype="bf16", extra_pages=7):
@@ -238,3 +239,55 @@ def test_config4_full_size_sampled(cuda):
     got = out.float().cpu().numpy()
     for (r, h), (rr, hh) in zip(samples, rows):
         check(got[r, h], exp[(rr, hh)], f"config4 row {r} head {h}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_prefill_score_jump_at_a_tiles_later_key(cuda, dtype):
+    """A key whose score is 16 (natural units), far above every earlier key's, at a key of its
+    32-key tile other than the first ones: the running max has to move to it, or its weight
+    (beyond 2^16 under the old max) overflows fp16. Every query row is the same vector u and a
+    jump key is gamma * u with gamma * scale * |u|^2 = 16, so it dominates each query that sees it. Sequence 0's jump key is prefix key
+    126 (tile 3, offset 30), sequence 1's chunk key 231 (tile 7, offset 7: seen from chunk
+    query 31 on). Both the plain and the statistics instance are checked against the oracle."""
+    import torch
+
+    from oracle import snapkv_oracle as so
+    from unifiedkv_amd import prefill, snapkv
+
+    case = make_case(11, [300, 200], [40, 96], dtype=dtype)
+    f = lambda a: oracle.bits_to_f32(a, workloads.DTYPE_CODES[dtype])
+    u = f(case["q"][0, 0])
+    case["q"][:] = case["q"][0, 0]
+    gamma = 16.0 / (case["scale"] * float(u @ u))
+    jump = workloads._round_bits((gamma * u).astype(np.float32), dtype)
+    case["k_cache"][case["block_table"][0][126 // 16], 126 % 16] = jump   # every KV head
+    case["k_new"][int(case["cu"][1]) + 31] = jump
+    k, _ = written_pool(case)
+    assert float(f(k[case["block_table"][0][7], 14, 0]) @ u) * case["scale"] > 15.5
+    exp = expected(case)
+    out, t = run_gpu(case, cuda)
+    got = out.float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    check(got, exp, f"score jump {dtype}")
+
+    # the statistics instance over the same pool (the chunk is written): output and rows
+    sink, obs = 4, 32
+    Hq, D = case["q"].shape[1], case["q"].shape[2]
+    st = snapkv.ObsStats(2, 1, Hq, sink_len=sink, obs_len=obs, softmax_scale=case["scale"], device=cuda)
+    out2 = prefill.paged_prefill_attention(t["q"], t["k_cache"], t["v_cache"], t["block_table"], t["cu"],
+                                           t["kv_lens"], softmax_scale=case["scale"], n_rep=case["n_rep"],
+                                           obs_stats=st, layer_id=0)
+    check(out2.float().cpu().numpy(), exp, f"score jump {dtype}, statistics instance")
+    rows = st.data.cpu().numpy()
+    for b in range(2):
+        L = int(case["kv_lens"][b])
+        Kd = f(k[case["block_table"][b]]).reshape(-1, k.shape[2], D)[:L].transpose(1, 0, 2)
+        Qo = f(case["q"][int(case["cu"][b + 1]) - obs:int(case["cu"][b + 1])]).transpose(1, 0, 2)
+        want = so.obs_row_stats(Kd, Qo, sink_len=sink, obs_len=obs, n_rep=case["n_rep"], scale=case["scale"])
+        assert np.all(rows[b, 0, :, :, 1] == 0)
+        # fp32 dot products of 128 terms summing to ~180 before scaling: the row's error bound
+        # is D * 2^-24 * sum|q_d k_d| * scale * log2(e), about 2e-4 here
+        bound = D * 2.0 ** -24 * float(np.abs(u * f(jump)).sum()) * case["scale"] / math.log(2) + LSE_TOL_JUMP
+        err = np.abs(rows[b, 0, :, :, 0] - want).max()
+        assert err <= bound, f"seq {b}: normaliser off by {err:.3e} > {bound:.3e}"

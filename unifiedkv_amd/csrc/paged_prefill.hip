@@ -434,7 +434,12 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       // The max of the packed weights with three-input fp16 maxima (v_pk_maximum3_f16): a NaN
       // weight makes the maximum NaN, whose pattern, like inf's, lies above the threshold.
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      auto hv = [&](int i) { return __builtin_bit_cast(h2, pa[i / 4][i % 4]); };
+      // (the element is copied out first: clang lowers __builtin_bit_cast of a vector element
+      // lvalue to a load of the vector's first element, whatever the index)
+      auto hv = [&](int i) {
+        const uint32_t w = pa[i / 4][i % 4];
+        return __builtin_bit_cast(h2, w);
+      };
       h2 mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(hv(0), hv(1)), hv(2));
 #pragma unroll
       for (int i = 3; i + 1 < 4 * CB; i += 2)
