@@ -917,10 +917,11 @@ def run_scores(args, dev):
     """Config 5's importance scores computed instead of given: SnapKV observation-window block
     scores for 32 layers x 8 sequences at ctx 32768 (sink 64, obs 128), K read from the pool.
 
-    Headline: the scores from the row statistics the prefill's final chunk produces (the
-    reference scores after the prefill, from the queries its prefill hook kept): score_blocks'
-    time plus the extra time of the 32 final-chunk prefill calls that make the statistics,
-    against both passes' FLOPs. The standalone two-pass call is reported beside it."""
+    Two ways to the same scores are timed: the standalone two-pass call, and the scores from the
+    row statistics the prefill's final chunk produces (the reference scores after the prefill,
+    from the queries its prefill hook kept): score_blocks' time plus the extra time of the 32
+    final-chunk prefill calls that make the statistics. The headline is the faster of the two,
+    against both passes' FLOPs either way; the other is reported beside it."""
     import numpy as np
     import torch
 
@@ -951,11 +952,14 @@ def run_scores(args, dev):
     extra_ms, plain_ms, st_ms, st_per, one, two = prefill_stats_leg(pool, table, lists, dev, args.seed, args.steps)
     st_kern_ms = sum(st_per) / len(st_per)
     eff_ms = st_ms + extra_ms
-    tflops = flops / (eff_ms * 1e-3) / 1e12
+    st_tflops = flops / (eff_ms * 1e-3) / 1e12
+    path = "statistics" if eff_ms < region_ms else "two_pass"
+    best_ms = min(eff_ms, region_ms)
+    tflops = flops / (best_ms * 1e-3) / 1e12
     rel = ((one - two).abs() / two.abs().clamp_min(1e-30)).max().item()
     log(f"[bench] scores from prefill statistics: {st_ms * 1e3:.1f} us per call + prefill extra "
         f"{extra_ms * 1e3:.1f} us over 32 layers (final-chunk prefill {plain_ms * 1e3:.1f} us) = "
-        f"{tflops:.1f} TFLOP/s; max rel diff to two passes {rel:.2e}")
+        f"{st_tflops:.1f} TFLOP/s; max rel diff to two passes {rel:.2e}; faster path: {path}")
     cpu = None
     if not args.no_cpu_baseline:
         # One KV head of one item (its 4 q heads x 128 queries over all 32576 mid keys), fp32 numpy.
@@ -978,13 +982,17 @@ def run_scores(args, dev):
                "seconds_per_sample_run": round(med, 4)}
     return {
         "metric": ("Config 5 SnapKV block scores (32 layers x 8 seqs x 32K, obs 128), attention-score TFLOP/s "
-                   "(row statistics from the final prefill chunk, its extra time counted)"),
+                   "(the faster of: two passes over the keys; one pass from the final prefill chunk's row "
+                   "statistics, that chunk's extra prefill time counted)"),
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(eff_ms, 5),
+        "ms_per_step": round(best_ms, 5),
+        "path": path,
+        "statistics_path": {"us": round(eff_ms * 1e3, 1), "tflops": round(st_tflops, 2),
+                            "frac": round(st_tflops / PEAK_BF16_TFLOPS, 4)},
         "score_call_us": round(st_ms * 1e3, 1),
         "prefill_extra_us_32_layers": round(extra_ms * 1e3, 1),
         "final_chunk_prefill_us_32_layers": round(plain_ms * 1e3, 1),

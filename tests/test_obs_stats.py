@@ -196,6 +196,7 @@ def _prefill(cuda, dtype, chunks, *, Hq, Hkv, layers, sink, obs, seed, q_fill=No
     ("bf16", 8, 8, 0, 48, [[1000, 500], [300, 48]]),  # n_rep 1, obs not a multiple of 16, no sink,
                                                       # a final chunk of exactly the window
     ("bf16", 32, 8, 16, 128, [[300, 2000]]),          # one chunk each
+    ("bf16", 32, 8, 64, 128, [[1280] * 8]),           # 8 x 8 groups: statistics, 96- and 64-query blocks
 ])
 def test_prefill_rows_match_oracle_and_outputs_match_plain_prefill(cuda, dtype, Hq, Hkv, sink, obs, chunks):
     layers = 2

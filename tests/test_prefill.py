@@ -181,6 +181,59 @@ def test_prefill_bf16_v_beyond_fp16_range(cuda, big):
 
 
 @pytest.mark.gpu
+def test_prefill_bf16_v_beyond_fp16_range_under_a_vanishing_weight(cuda):
+    """A bf16 V of 3e38 at a key whose weight (below 2^-30 of the running max's even when that
+    lags the largest score by the whole 2^8 allowance) rounds to zero in fp16: its true share,
+    ~1e-13 x 3e38, dominates those outputs, so the workgroup must still take the fp32 fallback
+    however small the key's fp16 weight is."""
+    case = make_case(78, [300, 40], [64, 25])
+    f = lambda a: oracle.bits_to_f32(a, oracle.DT_BF16)
+    u = f(case["q"][0, 0])
+    case["q"][:] = case["q"][0, 0]
+    low = workloads._round_bits((-24.0 / (case["scale"] * float(u @ u)) * u).astype(np.float32), "bf16")
+    page = case["block_table"][0][5]
+    case["k_cache"][page, 3] = low                       # prefix key 83 of sequence 0, every head
+    case["v_cache"][page, 3, 2, 7] = workloads._round_bits(np.array([3.0e38], np.float32), "bf16")[0]
+    exp = expected(case)
+    assert np.isfinite(exp).all() and np.abs(exp).max() > 1e20   # the vanishing weight's share shows
+    out, _ = run_gpu(case, cuda)
+    check(out.float().cpu().numpy(), exp, "bf16 V of 3e38 under a weight fp16 rounds to zero")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("chunk", [[640] * 8, [640, 600, 37, 640, 1, 640, 333, 0]])
+def test_prefill_block_plans_of_both_widths_sampled(cuda, chunk):
+    """8 sequences x 8 KV groups with chunks of up to 640 queries: on a 256-CU device the launch
+    plans four 96-query blocks (three column blocks per wave) and four 64-query blocks per
+    (sequence, group), anchored at each chunk's end, so shorter chunks leave partial and empty
+    blocks at their start. Sampled (query, head) pairs - both ends of every chunk, the queries
+    either side of each block boundary, random ones - against the fp64 oracle."""
+    import torch
+
+    prefix = [300, 0, 1000, 64, 17, 500, 2000, 5]
+    case = make_case(sum(chunk), prefix, chunk)
+    out, t = run_gpu(case, cuda)
+    got = out.float().cpu().numpy()
+    rng = np.random.default_rng(3)
+    rows = set()
+    for b, C in enumerate(chunk):
+        if C == 0:
+            continue
+        base = int(case["cu"][b])
+        edges = {0, C - 1}
+        for w in (4 * 96 + 64 * k for k in range(5)):  # block boundaries below the chunk's end
+            edges |= {C - w, C - w - 1}
+        edges |= {C - 96 * k for k in range(1, 5)} | {C - 96 * k - 1 for k in range(1, 5)}
+        for i in edges | set(rng.integers(0, C, 6).tolist()):
+            if 0 <= i < C:
+                rows.add((base + int(i), int(rng.integers(0, 32))))
+    rows = sorted(rows)
+    exp = expected(case, rows=rows)
+    for r, h in rows:
+        check(got[r, h], exp[(r, h)], f"chunks {chunk}: row {r} head {h}")
+
+
+@pytest.mark.gpu
 def test_prefill_last_row_matches_page16_decode(cuda):
     """The last query of a chunk sees exactly the decode step's keys."""
     import torch

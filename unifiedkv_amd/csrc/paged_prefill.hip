@@ -11,14 +11,18 @@
 // are read from 16-token pages through the block table, and
 // ukv_kv_write_varlen first writes the chunk's own K/V into its pages.
 //
-// Kernel: one workgroup of W waves (W = 8, two per SIMD) takes QW = W * 3 *
+// Kernel: one workgroup of W waves (W = 8, two per SIMD) takes QW = W * CB *
 // (16 / n_rep) consecutive queries of one KV group. Within a wave, an MFMA
 // column is a (query, q head) pair: 16 / n_rep queries times the n_rep q heads
-// of the group, so one K/V read serves the whole GQA group; a wave holds three
-// 16-column blocks.
-//   * workgroups are ordered so that each XCD (dispatch is round-robin over the
-//     8 XCDs) runs consecutive work items: the query blocks of one (sequence,
-//     group) share that XCD's L2 while they stream the same pages;
+// of the group, so one K/V read serves the whole GQA group; a wave holds CB
+// 16-column blocks, three or two.
+//   * block plan: the chunk of each (sequence, group) is cut from its end down
+//     into three-column blocks and then two-column ones (three are cheaper per
+//     query, two fill the last round of the launch: the host picks the mix that
+//     its model of the dispatch finishes first); each XCD (dispatch is
+//     round-robin over the 8 XCDs) runs a contiguous range of (sequence, group)
+//     pairs, three-column blocks first: the query blocks of one pair share that
+//     XCD's L2 while they stream the same pages;
 //   * key tiles of 32 keys (two pages) pass through registers into a 4-slot
 //     LDS ring (rows padded to 288 B), written two tiles ahead of their use,
 //     with a barrier after every second tile; the loads of tiles t+3 and t+4
@@ -37,12 +41,18 @@
 //     operands come from ds_read_b64_tr_b16 transpose reads; the softmax
 //     denominators come from one more MFMA against a ones operand, so they sum
 //     exactly the rounded P;
-//   * the STATS instance (the blocks holding each sequence's last obs queries,
-//     launched in the same grid) also sums the middle keys' fp32 weights into
-//     SnapKV's row statistics.
+//   * the STATS instance (two-column blocks holding each sequence's last obs
+//     queries, launched in the same grid) also sums the middle keys' fp32
+//     weights into SnapKV's row statistics.
 #include <algorithm>
-#include <type_traits>
 #include <cmath>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <queue>
+#include <tuple>
+#include <type_traits>
+#include <vector>
 
 #include "ukv_common.h"
 
@@ -59,7 +69,14 @@ struct PrefillArgs {
   const int32_t* bt;
   const int32_t* cu_q;     // [B+1]
   const int32_t* kv_lens;  // [B] keys per sequence, the chunk included
-  int B, Hq, n_rep, n_groups, D, max_blocks, num_pages, n_qblocks;
+  int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
+  // Query blocks of every (sequence, KV group), from the end of its chunk down: n_s blocks of two
+  // column blocks per wave that also write the statistics (obs > 0 only), then n3 blocks of three
+  // column blocks, then n2 of two. Blocks that reach below the chunk's first query are partial or
+  // empty (chunks shorter than the longest). The three-column blocks of every pair are dispatched
+  // in a first pass, the two-column ones in a second; the statistics blocks lead the first pass,
+  // or the second when stats_second is set.
+  int n_s, n3, n2, stats_second;
   float scale, scale_log2;
   // SnapKV observation statistics (obs > 0): the query blocks that hold a sequence's last obs
   // queries run in the STATS instance, which also writes, for each of those queries and q head
@@ -68,7 +85,7 @@ struct PrefillArgs {
   // (.y = 0, or 1 where the sum lost precision), the row statistics the SnapKV scoring pass takes.
   float2* obs_stats;
   int64_t stats_seq_stride;
-  int sink, obs, n_obs_blocks;
+  int sink, obs;
 };
 
 __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
@@ -124,7 +141,6 @@ constexpr int kTileKeys = 32;
 constexpr int kRowPad = UKV_PREFILL_KPAD;
 constexpr int kVRowPad = UKV_PREFILL_VPAD;
 constexpr int kStages = 4;  // K/V ring slots: tiles are written two ahead, a barrier every second tile
-constexpr int kColBlocks = 3;  // 16-column blocks per wave (3 measured 2.5 % faster than 2; 247 VGPRs)
 
 // Fallback for a workgroup whose key range holds a bf16 V value of magnitude
 // >= 65520 (or infinite), which fp16 cannot carry: every (query, head) pair
@@ -172,18 +188,19 @@ struct PrefillLds {
   __attribute__((aligned(16))) uint16_t v_s[kStages][kTileKeys][kVRowPad];
 };
 
-// Work item `item` of (sequence b, KV group g) of the tiled prefill. STATS: the blocks that
-// hold the sequence's last obs queries (two column blocks per wave), which also produce those
-// queries' SnapKV row statistics.
-template <int DT, int WAVES, bool STATS>
-__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, const int g, const int item,
+// The query block q0 .. q0 + QW - 1 (QW = WAVES * CB * 16 / n_rep; q0 may be negative) of
+// sequence b, KV group g, with CB 16-column blocks per wave. STATS: a block holding some of the
+// sequence's last obs queries (two column blocks per wave), which also produces those queries'
+// SnapKV row statistics.
+template <int DT, int WAVES, bool STATS, int CB>
+__device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, const int g, const int q0,
                                              PrefillLds& lds) {
   constexpr int D = 128;
   constexpr int STEPS = D / 32;
   constexpr int NT = 64 * WAVES;
   constexpr int ITEMS = kTileKeys * 16 / NT;  // 16-byte chunks per thread per tensor per tile
   // The STATS instance holds two column blocks, which leaves registers for its sums.
-  constexpr int CB = STATS ? 2 : kColBlocks;
+  static_assert(!STATS || CB == 2, "statistics blocks hold two column blocks per wave");
   constexpr float kTau = 8.f;
   constexpr bool kBf16 = DT == UKV_DTYPE_BF16;
   static_assert(ITEMS * NT == kTileKeys * 16, "loader mapping");
@@ -198,18 +215,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 
   const int qpb = 16 / a.n_rep;  // queries per column block
   const int qw = WAVES * CB * qpb;
-  // Queries from obs_q0(C) on run in the STATS instance when obs > 0: the main instance's
-  // query blocks from the one holding query C - obs.
-  const int qw_main = WAVES * kColBlocks * qpb;
-  auto obs_q0 = [&](int Cq) { return max(0, Cq - a.obs) / qw_main * qw_main; };
-  // item: the STATS block of the (sequence, group) (from query obs_q0(C) on), or its main
-  // query block, the longest first
-  const int q0 = STATS ? obs_q0(a.cu_q[b + 1] - a.cu_q[b]) + item * qw : (a.n_qblocks - 1 - item) * qw;
   const int q_begin = a.cu_q[b];
   const int C = a.cu_q[b + 1] - q_begin;
-  if (q0 >= C) return;  // whole workgroup
-  if constexpr (!STATS)
-    if (a.obs > 0 && q0 >= obs_q0(C)) return;  // the STATS instance's queries
+  if (q0 >= C || q0 + qw <= 0) return;  // whole workgroup
   const int Lk = kv_len_of(a, b);
   const int P0 = Lk - C;  // keys before the chunk
   const int kend = max(0, min(Lk, P0 + min(C, q0 + qw)));
@@ -218,16 +226,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 
   // This wave's queries and this lane's columns.
   const int wq0 = q0 + wv * CB * qpb;
-  const bool wave_live = wq0 < C;
+  const bool wave_live = wq0 < C && wq0 + CB * qpb > 0;
   const int wpos_min = P0 + wq0;
   const int head = g * a.n_rep + i16 % a.n_rep;
-  int qpos[CB];  // absolute position of the column's query, or -1 if the column is unused
+  // the query of this lane's column in column block cb is qi0 + cb * qpb (unused if outside 0 .. C - 1)
+  const int qi0 = wq0 + i16 / a.n_rep;
   u32x4 qv[CB][STEPS];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    const int qi = wq0 + cb * qpb + i16 / a.n_rep;
-    const bool live = qi < C && head < a.Hq;
-    qpos[cb] = live ? P0 + qi : -1;
+    const int qi = qi0 + cb * qpb;
+    const bool live = qi >= 0 && qi < C && head < a.Hq;
     const uint16_t* qp = a.q + (int64_t)(q_begin + (live ? qi : 0)) * a.q_st + (int64_t)(live ? head : 0) * a.q_sh +
                          8 * kg;
 #pragma unroll
@@ -358,7 +366,9 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       // key kb*16 + 4kg + r is visible to a column iff it is below lim[kb]
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        const int vis = min(Lk, qpos[cb] + 1) - key0 - 4 * kg;
+        const int qi = qi0 + cb * qpb;
+        const bool live = qi >= 0 && qi < C && head < a.Hq;
+        const int vis = live ? min(Lk, P0 + qi + 1) - key0 - 4 * kg : -1;  // an unused column sees no key
         const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis - 16 : 0;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -531,7 +541,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       l += __shfl_xor(l, 32);
       const int qi = wq0 + cb * qpb + i16 / a.n_rep;
       const int hh = g * a.n_rep + i16 % a.n_rep;
-      if (wave_live && kg == 0 && qi >= C - a.obs && qi < C && hh < a.Hq) {
+      if (wave_live && kg == 0 && qi >= C - a.obs && qi >= 0 && qi < C && hh < a.Hq) {
         const float m = m_ref[cb];
         const float top = n_pad > 0 ? fmaxf(m, 0.f) : m;
         const float lse = top + __log2f(l * exp2f(m - top) + (float)n_pad * exp2f(-top));
@@ -548,7 +558,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
   if (kBf16 && __syncthreads_or(wide_mine)) {
-    prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, q0, min(C, q0 + qw), wv, WAVES, lane);
+    prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, max(q0, 0), min(C, q0 + qw), wv, WAVES, lane);
     return;
   }
 
@@ -562,7 +572,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       const int col = 4 * kg + r;
       const int qi = wq0 + cb * qpb + col / a.n_rep;
       const int hh = g * a.n_rep + col % a.n_rep;
-      if (qi < C && hh < a.Hq) {
+      if (qi >= 0 && qi < C && hh < a.Hq) {
         const float inv = 1.f / lacc[cb][r];
         uint16_t* orow = a.out + ((int64_t)(q_begin + qi) * a.Hq + hh) * D + i16;
 #pragma unroll
@@ -572,27 +582,57 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   }
 }
 
-// Work items: for each (sequence, KV group), n_obs_blocks STATS blocks (WITH_STATS only;
-// they hold the longest queries) and then n_qblocks main query blocks, the longest first.
-// Each XCD (dispatch is round-robin over the 8 XCDs) takes a contiguous range of items, so
-// that the blocks of one (sequence, group) share that XCD's L2 while they stream its pages.
+// Work items: the n_s + n3 + n2 query blocks of each (sequence, KV group) ("pair"), numbered
+// pair after pair. Each XCD (dispatch is round-robin over the 8 XCDs) takes a contiguous range
+// of these numbers, so that the blocks of one pair share that XCD's L2 while they stream its
+// pages, and dispatches the statistics and three-column blocks of its pairs before their
+// two-column blocks: the cheaper blocks then fill the last round of the launch.
 template <int DT, int WAVES, bool WITH_STATS>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 paged_prefill_kernel(const PrefillArgs a) {
   __shared__ PrefillLds lds;
-  const int n_s = WITH_STATS ? a.n_obs_blocks : 0;
-  const int n_items = n_s + a.n_qblocks;
+  const int n_long = (WITH_STATS && a.stats_second) ? a.n3 : a.n_s + a.n3;  // items of the first pass
+  const int n_items = a.n_s + a.n3 + a.n2;
   const int total = n_items * a.n_groups * a.B;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int xcd = blockIdx.x & 7;
   const int per = total >> 3, rem = total & 7;
-  const int work = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + slot;
-  const int item = work % n_items;
-  const int pair = work / n_items;
+  const int start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+  const int end = start + per + (xcd < rem ? 1 : 0);
+  // this workgroup's place in the XCD's order: the long blocks of the range's pairs, pair by
+  // pair, then their two-column blocks
+  int s = blockIdx.x >> 3, pair = -1, j = 0;
+  for (int pass = 0; pass < 2 && pair < 0; ++pass) {
+    for (int p = start / n_items; p <= (end - 1) / n_items; ++p) {
+      const int j0 = max(pass ? n_long : 0, start - p * n_items);
+      const int j1 = min(pass ? n_items : n_long, end - p * n_items);
+      const int cnt = max(0, j1 - j0);
+      if (s < cnt) {
+        pair = p;
+        j = j0 + s;
+        break;
+      }
+      s -= cnt;
+    }
+  }
+  if (pair < 0) return;  // (the grid holds exactly total workgroups)
   const int g = pair % a.n_groups, b = pair / a.n_groups;
-  if (WITH_STATS && item < n_s)
-    prefill_tile<DT, WAVES, true>(a, b, g, item, lds);
-  else
-    prefill_tile<DT, WAVES, false>(a, b, g, item - n_s, lds);
+  const int C = a.cu_q[b + 1] - a.cu_q[b];
+  const int qpb = 16 / a.n_rep;
+  const int qw2 = WAVES * 2 * qpb, qw3 = WAVES * 3 * qpb;
+  // item j in dispatch order -> its block; blocks from the end of the chunk down: statistics,
+  // three-column, two-column
+  const int ns = WITH_STATS ? a.n_s : 0;
+  const bool second = WITH_STATS && a.stats_second;
+  const int js = second ? j - a.n3 : j;                    // index among the statistics blocks
+  const int j3 = second ? j : j - ns;                      // among the three-column blocks
+  const int j2 = j - ns - a.n3;                            // among the two-column blocks
+  if (WITH_STATS && js >= 0 && js < ns) {
+    prefill_tile<DT, WAVES, true, 2>(a, b, g, C - qw2 * (js + 1), lds);
+  } else if (j3 >= 0 && j3 < a.n3) {
+    prefill_tile<DT, WAVES, false, 3>(a, b, g, C - qw2 * ns - qw3 * (j3 + 1), lds);
+  } else {
+    prefill_tile<DT, WAVES, false, 2>(a, b, g, C - qw2 * ns - qw3 * a.n3 - qw2 * (j2 + 1), lds);
+  }
 }
 
 // Marks every observation row of the call as recomputed-by-the-scorer: (0, 1) at row
@@ -818,6 +858,96 @@ extern "C" int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const
 
 namespace {
 
+// Block plan of the tiled prefill: the numbers n3 and n2 of three- and two-column query blocks
+// per (sequence, KV group) that cover the max_chunk - n_s * qw2 queries below the statistics
+// blocks, and the pass the statistics blocks are dispatched in. A launch runs in rounds of one
+// block per CU; the plan with the shortest predicted launch is taken, modelling every block as
+// streaming equally many keys (a long prefix) at its measured cost relative to a three-column
+// block (two columns 0.79: single blocks timed over the same 32768 keys; statistics 1.1: what
+// full launches with forced plans give them), and each XCD's CUs as taking the XCD's blocks in
+// the kernel's order, each CU the next block once free.
+struct BlockPlan {
+  int n3, n2, stats_second;
+};
+
+double plan_makespan(int64_t pairs, int n_s, int n3, int n2, bool stats_second, int cus_per_xcd) {
+  const int n_items = n_s + n3 + n2;
+  const int n_long = stats_second ? n3 : n_s + n3;
+  auto cost = [&](int64_t j) {
+    if (stats_second) return j < n3 ? 1.0 : (j < n3 + n_s ? 1.1 : 0.79);
+    return j < n_s ? 1.1 : (j < n_s + n3 ? 1.0 : 0.79);
+  };
+  const int64_t total = pairs * n_items;
+  const int64_t per = total / 8, rem = total % 8;
+  double worst = 0.0;
+  std::vector<double> order;
+  for (int x = 0; x < 8; ++x) {
+    const int64_t start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+    const int64_t end = start + per + (x < rem ? 1 : 0);
+    if (end <= start) continue;
+    order.clear();
+    for (int pass = 0; pass < 2; ++pass)
+      for (int64_t p = start / n_items; p <= (end - 1) / n_items; ++p) {
+        const int64_t j0 = std::max<int64_t>(pass ? n_long : 0, start - p * n_items);
+        const int64_t j1 = std::min<int64_t>(pass ? n_items : n_long, end - p * n_items);
+        for (int64_t j = j0; j < j1; ++j) order.push_back(cost(j));
+      }
+    std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
+    for (int c = 0; c < cus_per_xcd; ++c) cu.push(0.0);
+    double last = 0.0;
+    for (double c : order) {
+      const double t = cu.top() + c;
+      cu.pop();
+      cu.push(t);
+      last = std::max(last, t);
+    }
+    worst = std::max(worst, last);
+  }
+  return worst;
+}
+
+BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int n_s, int cus_per_xcd) {
+  const int left = std::max(0, max_chunk - n_s * qw2);
+  const int n3_max = (left + qw3 - 1) / qw3;
+  BlockPlan best{n3_max, 0, 0};
+  // Large launches run many rounds, where the last one matters little: keep three-column blocks.
+  if (pairs * (n3_max + n_s) > (1 << 16) || cus_per_xcd <= 0) return best;
+  static std::mutex mu;
+  static std::map<std::tuple<int, int64_t, int, int, int>, BlockPlan> cache;
+  const auto key = std::make_tuple(max_chunk, pairs, qw2, n_s, cus_per_xcd);
+  std::lock_guard<std::mutex> lock(mu);
+  const auto hit = cache.find(key);
+  if (hit != cache.end()) return hit->second;
+  double best_t = plan_makespan(pairs, n_s, n3_max, 0, false, cus_per_xcd);
+  // Each three-column block traded for two-column ones adds work (0.79 x 1.5 > 1): a dozen
+  // trades fill any last round.
+  for (int n3 = n3_max; n3 >= std::max(0, n3_max - 12); --n3) {
+    const int n2 = (left - n3 * qw3 + qw2 - 1) / qw2;
+    for (int second = 0; second <= (n_s > 0 ? 1 : 0); ++second) {
+      const double t = plan_makespan(pairs, n_s, n3, n2, second != 0, cus_per_xcd);
+      if (t < best_t - 1e-9) {
+        best_t = t;
+        best = BlockPlan{n3, n2, second};
+      }
+    }
+  }
+  cache.emplace(key, best);
+  return best;
+}
+
+// CUs per XCD of the current device (8 XCDs), 0 when unknown.
+int cus_per_xcd() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n / 8;
+  }
+  return cached[dev];
+}
+
 struct ObsStats {
   void* stats;
   int64_t seq_stride;
@@ -884,24 +1014,24 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
   }
   if (fast) {
     constexpr int W = UKV_PREFILL_WAVES;
-    const int qw = W * kColBlocks * (16 / n_rep);
-    a.n_qblocks = (max_chunk + qw - 1) / qw;
-    const int64_t wgs = (int64_t)a.n_qblocks * n_groups * batch;
+    const int qw2 = W * 2 * (16 / n_rep), qw3 = W * 3 * (16 / n_rep);
+    const int64_t pairs = (int64_t)n_groups * batch;
+    // the statistics blocks cover the last obs queries
+    a.n_s = obs ? (a.obs + qw2 - 1) / qw2 : 0;
+    const BlockPlan plan = choose_plan(max_chunk, pairs, qw2, qw3, a.n_s, cus_per_xcd());
+    a.n3 = plan.n3;
+    a.n2 = plan.n2;
+    a.stats_second = plan.stats_second;
+    const int64_t wgs = (int64_t)(a.n_s + a.n3 + a.n2) * pairs;
     if (wgs == 0) return UKV_OK;
+    if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
+    const dim3 grid((unsigned)wgs);
     if (!obs) {
-      if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
       if (dtype == UKV_DTYPE_BF16)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), grid, dim3(64 * W), 0, stream, a);
       else
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), grid, dim3(64 * W), 0, stream, a);
     } else {
-      // The STATS blocks (2 column blocks per wave) cover queries obs_q0 .. C - 1, fewer
-      // than obs + qw of them.
-      const int qw_stats = W * 2 * (16 / n_rep);
-      a.n_obs_blocks = (a.obs + qw - 1 + qw_stats - 1) / qw_stats;
-      const int64_t swgs = (int64_t)a.n_obs_blocks * n_groups * batch;
-      if (swgs + wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
-      const dim3 grid((unsigned)(swgs + wgs));
       if (dtype == UKV_DTYPE_BF16)
         hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), grid, dim3(64 * W), 0, stream, a);
       else
