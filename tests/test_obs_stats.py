@@ -197,6 +197,8 @@ def _prefill(cuda, dtype, chunks, *, Hq, Hkv, layers, sink, obs, seed, q_fill=No
                                                       # a final chunk of exactly the window
     ("bf16", 32, 8, 16, 128, [[300, 2000]]),          # one chunk each
     ("bf16", 32, 8, 64, 128, [[1280] * 8]),           # 8 x 8 groups: statistics, 96- and 64-query blocks
+    ("bf16", 8, 8, 16, 64, [[1536] * 8]),             # n_rep 1: statistics, 384- and 256-query blocks
+    ("fp16", 32, 4, 32, 64, [[512] * 8]),             # n_rep 8: statistics, 48- and 32-query blocks
 ])
 def test_prefill_rows_match_oracle_and_outputs_match_plain_prefill(cuda, dtype, Hq, Hkv, sink, obs, chunks):
     layers = 2

@@ -201,19 +201,22 @@ def test_prefill_bf16_v_beyond_fp16_range_under_a_vanishing_weight(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("chunk", [[640] * 8, [640, 600, 37, 640, 1, 640, 333, 0]])
-def test_prefill_block_plans_of_both_widths_sampled(cuda, chunk):
-    """8 sequences x 8 KV groups with chunks of up to 640 queries: on a 256-CU device the launch
-    plans four 96-query blocks (three column blocks per wave) and four 64-query blocks per
-    (sequence, group), anchored at each chunk's end, so shorter chunks leave partial and empty
-    blocks at their start. Sampled (query, head) pairs - both ends of every chunk, the queries
-    either side of each block boundary, random ones - against the fp64 oracle."""
-    import torch
-
+@pytest.mark.parametrize("Hq,Hkv,chunk", [
+    (32, 8, [640] * 8),                              # 4 + 4 blocks of 96 / 64 queries per pair
+    (32, 8, [640, 600, 37, 640, 1, 640, 333, 0]),    # the same plan over ragged chunks
+    (32, 2, [600] * 8),                              # n_rep 16: 16 + 14 blocks of 24 / 16 queries
+    (16, 1, [1024, 1000, 512, 1024, 7, 1024, 900, 1024]),  # n_rep 16, one KV head: 32 + 16
+])
+def test_prefill_block_plans_of_both_widths_sampled(cuda, Hq, Hkv, chunk):
+    """Multi-round launches whose block plan (on a 256-CU device) mixes blocks of three and two
+    column blocks per wave, anchored at each chunk's end, so shorter chunks leave partial and
+    empty blocks at their start. Sampled (query, head) pairs - both ends of every chunk, the
+    queries either side of the block boundaries, random ones - against the fp64 oracle."""
     prefix = [300, 0, 1000, 64, 17, 500, 2000, 5]
-    case = make_case(sum(chunk), prefix, chunk)
+    case = make_case(sum(chunk) + Hq, prefix, chunk, Hq=Hq, Hkv=Hkv)
     out, t = run_gpu(case, cuda)
     got = out.float().cpu().numpy()
+    qpb = 16 // (Hq // Hkv)
     rng = np.random.default_rng(3)
     rows = set()
     for b, C in enumerate(chunk):
@@ -221,16 +224,17 @@ def test_prefill_block_plans_of_both_widths_sampled(cuda, chunk):
             continue
         base = int(case["cu"][b])
         edges = {0, C - 1}
-        for w in (4 * 96 + 64 * k for k in range(5)):  # block boundaries below the chunk's end
-            edges |= {C - w, C - w - 1}
-        edges |= {C - 96 * k for k in range(1, 5)} | {C - 96 * k - 1 for k in range(1, 5)}
+        for w in (8 * 3 * qpb, 8 * 2 * qpb):  # boundaries of either block width below the chunk's end
+            for k in range(1, C // w + 1):
+                if k % 3 == 1:
+                    edges |= {C - k * w, C - k * w - 1}
         for i in edges | set(rng.integers(0, C, 6).tolist()):
             if 0 <= i < C:
-                rows.add((base + int(i), int(rng.integers(0, 32))))
+                rows.add((base + int(i), int(rng.integers(0, Hq))))
     rows = sorted(rows)
     exp = expected(case, rows=rows)
     for r, h in rows:
-        check(got[r, h], exp[(r, h)], f"chunks {chunk}: row {r} head {h}")
+        check(got[r, h], exp[(r, h)], f"Hq={Hq} Hkv={Hkv} chunks {chunk}: row {r} head {h}")
 
 
 @pytest.mark.gpu
