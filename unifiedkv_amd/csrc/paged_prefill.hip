@@ -582,6 +582,39 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   }
 }
 
+// The s-th work item an XCD dispatches from its range [start, end) of pair-major item numbers
+// (item j of pair p is number p * n + j): first the items j < nl of the range's pairs, pair by
+// pair, then the items j >= nl. Returns false past the range.
+__device__ __forceinline__ bool locate_item(int start, int end, int n, int nl, int s, int& pair, int& j) {
+  const int p0 = start / n, p1 = (end - 1) / n;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int lo = pass ? nl : 0, hi = pass ? n : nl, w = hi - lo;  // the pass's item numbers in a pair
+    const int c0 = max(0, min(hi, end - p0 * n) - max(lo, start - p0 * n));  // first pair, cut by start
+    if (s < c0) {
+      pair = p0;
+      j = max(lo, start - p0 * n) + s;
+      return true;
+    }
+    s -= c0;
+    if (p1 == p0) continue;
+    const int whole = max(0, p1 - p0 - 1);  // pairs wholly in the range
+    if (s < whole * w) {
+      pair = p0 + 1 + s / w;
+      j = lo + s % w;
+      return true;
+    }
+    s -= whole * w;
+    const int c1 = max(0, min(hi, end - p1 * n) - lo);  // last pair, cut by end
+    if (s < c1) {
+      pair = p1;
+      j = lo + s;
+      return true;
+    }
+    s -= c1;
+  }
+  return false;
+}
+
 // Work items: the n_s + n3 + n2 query blocks of each (sequence, KV group) ("pair"), numbered
 // pair after pair. Each XCD (dispatch is round-robin over the 8 XCDs) takes a contiguous range
 // of these numbers, so that the blocks of one pair share that XCD's L2 while they stream its
@@ -598,23 +631,8 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int per = total >> 3, rem = total & 7;
   const int start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
   const int end = start + per + (xcd < rem ? 1 : 0);
-  // this workgroup's place in the XCD's order: the long blocks of the range's pairs, pair by
-  // pair, then their two-column blocks
-  int s = blockIdx.x >> 3, pair = -1, j = 0;
-  for (int pass = 0; pass < 2 && pair < 0; ++pass) {
-    for (int p = start / n_items; p <= (end - 1) / n_items; ++p) {
-      const int j0 = max(pass ? n_long : 0, start - p * n_items);
-      const int j1 = min(pass ? n_items : n_long, end - p * n_items);
-      const int cnt = max(0, j1 - j0);
-      if (s < cnt) {
-        pair = p;
-        j = j0 + s;
-        break;
-      }
-      s -= cnt;
-    }
-  }
-  if (pair < 0) return;  // (the grid holds exactly total workgroups)
+  int pair, j;
+  if (!locate_item(start, end, n_items, n_long, blockIdx.x >> 3, pair, j)) return;  // (never: the grid holds total)
   const int g = pair % a.n_groups, b = pair / a.n_groups;
   const int C = a.cu_q[b + 1] - a.cu_q[b];
   const int qpb = 16 / a.n_rep;
