@@ -949,6 +949,7 @@ BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int n_s, i
       }
     }
   }
+  if (cache.size() >= 4096) cache.clear();  // a caller cycling through many shapes recomputes
   cache.emplace(key, best);
   return best;
 }
