@@ -202,6 +202,39 @@ def _sink_row(q, dt, D):
 
 
 @pytest.mark.parametrize("seed", range(16))
+def test_random_decode_hard_scores(cuda, seed):
+    """test_random_decode's layouts under the profiles of the hard prefill sweep below: jump
+    (1 in 200 key rows x8), sink (each sequence's first key along the queries' mean
+    direction), sharp (queries x4), bigv (values x1000; compared in units of that scale)."""
+    from unifiedkv_amd.page16_native import page16_decode_attention
+
+    rng = np.random.default_rng(7000 + seed)
+    kind = PROFILES[seed % len(PROFILES)]
+    dt, Hkv, n_rep, D, B, lens, bt, N = _decode_layout(rng, append=False)
+    Hq = Hkv * n_rep
+    q, k, v = _bits(rng, (B, Hq, D), dt), _bits(rng, (N, 16, Hkv, D), dt), _bits(rng, (N, 16, Hkv, D), dt)
+    if kind == "jump":
+        flat = k.reshape(-1, D)
+        idx = rng.choice(flat.shape[0], size=max(1, flat.shape[0] // 200), replace=False)
+        flat[idx] = _scaled(flat[idx], 8.0, dt)
+    elif kind == "sink":
+        row = _sink_row(q, dt, D)
+        for b in range(B):
+            if lens[b] > 0 and 0 <= bt[b, 0] < N:
+                k[bt[b, 0], 0] = row
+    elif kind == "sharp":
+        q = _scaled(q, 4.0, dt)
+    else:
+        v = _scaled(v, 1000.0, dt)
+    scale = 1.0 / math.sqrt(D)
+    out = page16_decode_attention(_up(q, dt), _up(k, dt), _up(v, dt), _i32(bt), _i32(lens), softmax_scale=scale,
+                                  n_rep=n_rep)
+    want = oracle.page16_decode_dense(_f(q, dt), _f(k, dt), _f(v, dt), bt, lens, softmax_scale=scale, n_rep=n_rep)
+    vscale = 1000.0 if kind == "bigv" else 1.0
+    _check(out.float().cpu().numpy() / vscale, want / vscale, f"seed {seed} {kind} {dt} B={B} Hq={Hq} Hkv={Hkv} D={D}")
+
+
+@pytest.mark.parametrize("seed", range(16))
 def test_random_prefill_hard_scores(cuda, seed):
     """test_random_prefill's layouts at D = 128 (the tiled kernel) under harder score profiles,
     chunks long enough for several tiles and both block widths:
