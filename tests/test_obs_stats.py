@@ -199,6 +199,9 @@ def _prefill(cuda, dtype, chunks, *, Hq, Hkv, layers, sink, obs, seed, q_fill=No
     ("bf16", 32, 8, 64, 128, [[1280] * 8]),           # 8 x 8 groups: statistics, 96- and 64-query blocks
     ("bf16", 8, 8, 16, 64, [[1536] * 8]),             # n_rep 1: statistics, 384- and 256-query blocks
     ("fp16", 32, 4, 32, 64, [[512] * 8]),             # n_rep 8: statistics, 48- and 32-query blocks
+    # n_rep 16: plans that dispatch the statistics blocks with the two-column ones (second pass)
+    ("bf16", 128, 8, 16, 64, [[128] * 14]),
+    ("fp16", 128, 8, 0, 32, [[96] * 13]),
 ])
 def test_prefill_rows_match_oracle_and_outputs_match_plain_prefill(cuda, dtype, Hq, Hkv, sink, obs, chunks):
     layers = 2
