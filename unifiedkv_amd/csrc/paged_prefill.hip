@@ -45,6 +45,7 @@
 //     queries, launched in the same grid) also sums the middle keys' fp32
 //     weights into SnapKV's row statistics.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <functional>
 #include <map>
@@ -956,15 +957,17 @@ BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int n_s, i
 
 // CUs per XCD of the current device (8 XCDs), 0 when unknown.
 int cus_per_xcd() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
+  int per = cached[dev].load(std::memory_order_relaxed);
+  if (per == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n / 8;
+    per = n / 8;
+    cached[dev].store(per, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return per;
 }
 
 struct ObsStats {
