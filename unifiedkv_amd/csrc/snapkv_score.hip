@@ -334,6 +334,9 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
           if constexpr (SCORES)
             if (j == 0 && ti > t0) head_sum(ti - 1, buf ^ 1);
           f32x4(&sc)[2] = acc[j & 1];
+          // The step's weights run at raised wave priority, lowered again for their column-sum
+          // MFMA (two-pass call ~1 % faster at config 5, from the first pass).
+          __builtin_amdgcn_s_setprio(1);
           if constexpr (SCORES) {
             // Weights times 2^kLift2 as fp16, dword 2*c2 + r/2 = rows r, r+1 of
             // column tile 2*half + c2 (k = the lane group's rows); the selector
@@ -349,6 +352,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
                 const float p1 = fast_exp2(__builtin_fmaf(sc[c2][r + 1], c, -m[k][r + 1]));
                 pk[2 * c2 + r / 2] = pack_f16(p0, p1);
               }
+            __builtin_amdgcn_s_setprio(0);
             colsum[hf] = mfma16x16x32<UKV_DTYPE_F16>(colsel, u32x4{pk[0], pk[1], pk[2], pk[3]}, colsum[hf]);
           } else {
             // Weights of the lane's 8 keys under the column's current max, times
@@ -394,6 +398,7 @@ __global__ void __launch_bounds__(64 * kSnapWaves, 2) snap_tile_kernel(const Sna
               weights(m[k][0]);
             }
             // Column sums on the matrix cores: every row of ones x P is the sum.
+            __builtin_amdgcn_s_setprio(0);
             lsum[k] = mfma16x16x32<UKV_DTYPE_F16>(ones, u32x4{pk[0], pk[1], pk[2], pk[3]}, lsum[k]);
           }
           // At most two steps' scores in flight: the next step starts here.
