@@ -334,6 +334,12 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  * The reference captures the window's queries in its q_proj hook (core/scheduler.py:269-341)
  * and normalises their softmax over K_mid at selection time (core/scheduler.py:565-592,
  * core/compress.py:116-130); here that normaliser is taken while the prefill streams the keys.
+ * The query blocks that hold the window run in a second kernel, beside the prefill kernel, on a
+ * library-owned stream of the current device (default priority) that the call forks from the given
+ * stream and joins back into it with events: work enqueued on the given stream after the call sees
+ * every result, and a call captured into a HIP graph records both kernels. The device's first such
+ * call creates that stream and its two events (held until the process ends); make it outside graph
+ * capture. Calls from several host threads on one device are serialised around the fork and join.
  */
 int ukv_paged_prefill_obs_stats(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                                 const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch,

@@ -202,6 +202,8 @@ def _prefill(cuda, dtype, chunks, *, Hq, Hkv, layers, sink, obs, seed, q_fill=No
     # n_rep 16: plans that dispatch the statistics blocks with the two-column ones (second pass)
     ("bf16", 128, 8, 16, 64, [[128] * 14]),
     ("fp16", 128, 8, 0, 32, [[96] * 13]),
+    # a final chunk of exactly the statistics blocks' 128 queries: the statistics kernel alone
+    ("bf16", 32, 8, 16, 128, [[1000, 800], [128, 128]]),
 ])
 def test_prefill_rows_match_oracle_and_outputs_match_plain_prefill(cuda, dtype, Hq, Hkv, sink, obs, chunks):
     layers = 2
@@ -254,6 +256,79 @@ def test_scores_from_prefill_rows_match_two_pass_and_oracle(cuda, dtype):
             got = one[b * layers + layer]
             err = np.abs(got - want)
             assert np.all(err <= 1e-4 * np.abs(want).max() + 1e-3 * np.abs(want)), (b, layer, err.max())
+
+
+def _side_stream_case(cuda):
+    """A final chunk whose statistics blocks run beside the prefill kernel's (both launches)."""
+    import torch
+
+    from unifiedkv_amd import snapkv
+    from unifiedkv_amd.prefill import paged_prefill_attention
+
+    B, P, C, Hq, Hkv, D, sink, obs = 4, 1500, 700, 32, 8, 128, 16, 128
+    g = torch.Generator(device=cuda)
+    g.manual_seed(5)
+    per = -(-(P + C) // 16)
+    N = B * per + 8
+    bt = torch.randperm(N, generator=g, device=cuda)[:B * per].view(B, per).to(torch.int32)
+    mk = lambda *shape: torch.randn(shape, generator=g, device=cuda).to(torch.bfloat16)  # noqa: E731
+    kc, vc = mk(N, 16, Hkv, D), mk(N, 16, Hkv, D)
+    qs = [mk(B * C, Hq, D) for _ in range(4)]
+    cu = torch.arange(0, B * C + 1, C, dtype=torch.int32, device=cuda)
+    lens = torch.full((B,), P + C, dtype=torch.int32, device=cuda)
+    stats = lambda: snapkv.ObsStats(B, 1, Hq, sink_len=sink, obs_len=obs, softmax_scale=D ** -0.5,  # noqa: E731
+                                    device=cuda)
+
+    def call(q, st):
+        return paged_prefill_attention(q, kc, vc, bt, cu, lens, softmax_scale=D ** -0.5, n_rep=Hq // Hkv,
+                                       max_chunk=C, obs_stats=st, layer_id=0, host_lens=([C] * B, [P + C] * B))
+    return qs, stats, call
+
+
+@pytest.mark.gpu
+def test_prefill_with_statistics_replays_from_a_captured_graph(cuda):
+    """The statistics kernel runs on a side stream forked from the caller's and joined back into
+    it: a captured graph holds both launches, and each replay (new queries copied in, eager calls
+    and synchronisations between replays) equals the eager call bit for bit."""
+    import torch
+
+    qs, stats, call = _side_stream_case(cuda)
+    st_g, st_e = stats(), stats()
+    q = qs[0].clone()
+    call(q, st_g)  # the device's side stream is created at its first statistics call, outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = call(q, st_g)
+    for i in (1, 2, 3):
+        q.copy_(qs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        want = call(qs[i], st_e)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, want), f"replay {i}: attention output"
+        assert torch.equal(st_g.data, st_e.data), f"replay {i}: statistics"
+
+
+@pytest.mark.gpu
+def test_prefill_with_statistics_orders_the_callers_stream(cuda):
+    """On a caller's own stream, work queued after the call sees both kernels' results (the join
+    makes that stream wait for the side stream)."""
+    import torch
+
+    qs, stats, call = _side_stream_case(cuda)
+    st_e, st_s = stats(), stats()
+    want = call(qs[1], st_e)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        st_s.data.fill_(float("nan"))
+        out = call(qs[1], st_s)
+        got_out, got_st = out.clone(), st_s.data.clone()  # queued right behind the call
+    s.synchronize()
+    assert torch.equal(got_out, want)
+    assert torch.equal(got_st, st_e.data)
 
 
 @pytest.mark.gpu

@@ -41,9 +41,10 @@
 //     operands come from ds_read_b64_tr_b16 transpose reads; the softmax
 //     denominators come from one more MFMA against a ones operand, so they sum
 //     exactly the rounded P;
-//   * the STATS instance (two-column blocks holding each sequence's last obs
-//     queries, launched in the same grid) also sums the middle keys' fp32
-//     weights into SnapKV's row statistics.
+//   * SnapKV row statistics: the two-column blocks holding each sequence's
+//     last obs queries run in a kernel of their own (paged_prefill_stats_kernel),
+//     which also sums the middle keys' fp32 weights; it runs beside the prefill
+//     kernel on a side stream forked from and joined back into the caller's.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -71,16 +72,16 @@ struct PrefillArgs {
   const int32_t* cu_q;     // [B+1]
   const int32_t* kv_lens;  // [B] keys per sequence, the chunk included
   int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
-  // Query blocks of every (sequence, KV group), from the end of its chunk down: n_s blocks of two
-  // column blocks per wave that also write the statistics (obs > 0 only), then n3 blocks of three
-  // column blocks, then n2 of two. Blocks that reach below the chunk's first query are partial or
-  // empty (chunks shorter than the longest). The three-column blocks of every pair are dispatched
-  // in a first pass, the two-column ones in a second; the statistics blocks lead the first pass,
-  // or the second when stats_second is set.
-  int n_s, n3, n2, stats_second;
+  // Query blocks of every (sequence, KV group), from q_skip queries below the end of its chunk
+  // down: n3 blocks of three column blocks per wave, then n2 of two. Blocks that reach below the
+  // chunk's first query are partial or empty (chunks shorter than the longest). The three-column
+  // blocks of every pair are dispatched in a first pass, the two-column ones in a second. With
+  // statistics (obs > 0), the last q_skip = n_s * (two-column block) queries of each chunk are the
+  // n_s blocks of the statistics kernel, launched beside it.
+  int n3, n2, q_skip, n_s;
   float scale, scale_log2;
   // SnapKV observation statistics (obs > 0): the query blocks that hold a sequence's last obs
-  // queries run in the STATS instance, which also writes, for each of those queries and q head
+  // queries run in the statistics kernel, which also writes, for each of those queries and q head
   // h, the log2-sum-exp2 of its scaled scores over the middle keys [sink, L - obs) and the zero
   // rows that pad them to a multiple of 16 keys: obs_stats[b * stats_seq_stride + h * obs + i].x
   // (.y = 0, or 1 where the sum lost precision), the row statistics the SnapKV scoring pass takes.
@@ -622,42 +623,59 @@ __device__ __forceinline__ bool locate_item(int start, int end, int n, int nl, i
   return false;
 }
 
-// Work items: the n_s + n3 + n2 query blocks of each (sequence, KV group) ("pair"), numbered
-// pair after pair. Each XCD (dispatch is round-robin over the 8 XCDs) takes a contiguous range
-// of these numbers, so that the blocks of one pair share that XCD's L2 while they stream its
-// pages, and dispatches the statistics and three-column blocks of its pairs before their
-// two-column blocks: the cheaper blocks then fill the last round of the launch.
-template <int DT, int WAVES, bool WITH_STATS>
+// The range of work items [start, end) of a launch's n_items items that XCD xcd runs: dispatch
+// is round-robin over the 8 XCDs, so the workgroups with blockIdx.x % 8 == xcd run there, and
+// each XCD takes a contiguous range of the item numbers.
+__device__ __forceinline__ void xcd_range(int total, int xcd, int& start, int& end) {
+  const int per = total >> 3, rem = total & 7;
+  start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+  end = start + per + (xcd < rem ? 1 : 0);
+}
+
+// Work items: the n3 + n2 query blocks of each (sequence, KV group) ("pair"), numbered pair
+// after pair. Each XCD takes a contiguous range of these numbers, so that the blocks of one pair
+// share that XCD's L2 while they stream its pages, and dispatches the three-column blocks of its
+// pairs before their two-column blocks: the cheaper blocks then fill the last round of the launch.
+// SKIP: the blocks end q_skip queries below each chunk's end, where the statistics kernel's blocks
+// take over. (Launches without statistics take the instance without it, whose two-column loop the
+// compiler schedules better: the unknown q_skip cost those blocks ~4 %.)
+template <int DT, int WAVES, bool SKIP>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 paged_prefill_kernel(const PrefillArgs a) {
   __shared__ PrefillLds lds;
-  const int n_long = (WITH_STATS && a.stats_second) ? a.n3 : a.n_s + a.n3;  // items of the first pass
-  const int n_items = a.n_s + a.n3 + a.n2;
-  const int total = n_items * a.n_groups * a.B;
-  const int xcd = blockIdx.x & 7;
-  const int per = total >> 3, rem = total & 7;
-  const int start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
-  const int end = start + per + (xcd < rem ? 1 : 0);
-  int pair, j;
-  if (!locate_item(start, end, n_items, n_long, blockIdx.x >> 3, pair, j)) return;  // (never: the grid holds total)
+  const int n_items = a.n3 + a.n2;
+  int start, end, pair, j;
+  xcd_range(n_items * a.n_groups * a.B, blockIdx.x & 7, start, end);
+  if (!locate_item(start, end, n_items, a.n3, blockIdx.x >> 3, pair, j)) return;  // (never: the grid holds total)
   const int g = pair % a.n_groups, b = pair / a.n_groups;
-  const int C = a.cu_q[b + 1] - a.cu_q[b];
+  const int top = a.cu_q[b + 1] - a.cu_q[b] - (SKIP ? a.q_skip : 0);  // the blocks end here
   const int qpb = 16 / a.n_rep;
   const int qw2 = WAVES * 2 * qpb, qw3 = WAVES * 3 * qpb;
-  // item j in dispatch order -> its block; blocks from the end of the chunk down: statistics,
-  // three-column, two-column
-  const int ns = WITH_STATS ? a.n_s : 0;
-  const bool second = WITH_STATS && a.stats_second;
-  const int js = second ? j - a.n3 : j;                    // index among the statistics blocks
-  const int j3 = second ? j : j - ns;                      // among the three-column blocks
-  const int j2 = j - ns - a.n3;                            // among the two-column blocks
-  if (WITH_STATS && js >= 0 && js < ns) {
-    prefill_tile<DT, WAVES, true, 2>(a, b, g, C - qw2 * (js + 1), lds);
-  } else if (j3 >= 0 && j3 < a.n3) {
-    prefill_tile<DT, WAVES, false, 3>(a, b, g, C - qw2 * ns - qw3 * (j3 + 1), lds);
-  } else {
-    prefill_tile<DT, WAVES, false, 2>(a, b, g, C - qw2 * ns - qw3 * a.n3 - qw2 * (j2 + 1), lds);
-  }
+  if (j < a.n3)
+    prefill_tile<DT, WAVES, false, 3>(a, b, g, top - qw3 * (j + 1), lds);
+  else
+    prefill_tile<DT, WAVES, false, 2>(a, b, g, top - qw3 * a.n3 - qw2 * (j - a.n3 + 1), lds);
+}
+
+// The statistics blocks: the n_s two-column blocks at the end of each pair's chunk, which hold
+// its last obs queries. A kernel of their own, launched beside paged_prefill_kernel: built into
+// one kernel, the statistics code changed the compiler's register allocation and schedule of the
+// three-column blocks' loop, which then ran ~10 % slower. Each XCD runs the statistics blocks of
+// the pairs whose other blocks it runs in paged_prefill_kernel (for the same number of pairs), so
+// both read a pair's pages through one L2.
+template <int DT, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+paged_prefill_stats_kernel(const PrefillArgs a) {
+  __shared__ PrefillLds lds;
+  int start, end;
+  xcd_range(a.n_s * a.n_groups * a.B, blockIdx.x & 7, start, end);
+  const int item = start + (blockIdx.x >> 3);
+  if (item >= end) return;  // (never: the grid holds total)
+  const int pair = item / a.n_s, js = item % a.n_s;
+  const int g = pair % a.n_groups, b = pair / a.n_groups;
+  const int C = a.cu_q[b + 1] - a.cu_q[b];
+  const int qw2 = WAVES * 2 * (16 / a.n_rep);
+  prefill_tile<DT, WAVES, true, 2>(a, b, g, C - qw2 * (js + 1), lds);
 }
 
 // Marks every observation row of the call as recomputed-by-the-scorer: (0, 1) at row
@@ -884,39 +902,34 @@ extern "C" int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const
 namespace {
 
 // Block plan of the tiled prefill: the numbers n3 and n2 of three- and two-column query blocks
-// per (sequence, KV group) that cover the max_chunk - n_s * qw2 queries below the statistics
-// blocks, and the pass the statistics blocks are dispatched in. A launch runs in rounds of one
-// block per CU; the plan with the shortest predicted launch is taken, modelling every block as
-// streaming equally many keys (a long prefix) at its measured cost relative to a three-column
-// block (two columns 0.79: single blocks timed over the same 32768 keys; statistics 1.1: what
-// full launches with forced plans give them), and each XCD's CUs as taking the XCD's blocks in
-// the kernel's order, each CU the next block once free.
+// per (sequence, KV group) that cover its chunk's max_chunk queries (those below the statistics
+// blocks). A launch runs in rounds of one block per CU; the plan with the shortest predicted
+// launch is taken, modelling every block as streaming equally many keys (a long prefix) at its
+// measured cost relative to a three-column block (two columns 0.79: single blocks timed over the
+// same 32768 keys; statistics blocks 0.84: launches with forced plans), and each XCD's CUs as
+// taking the XCD's blocks in the kernel's order, each CU the next block once free, after the n_s
+// statistics blocks per pair that the statistics kernel (launched first, beside it) puts there.
 struct BlockPlan {
-  int n3, n2, stats_second;
+  int n3, n2;
 };
 
-double plan_makespan(int64_t pairs, int n_s, int n3, int n2, bool stats_second, int cus_per_xcd) {
-  const int n_items = n_s + n3 + n2;
-  const int n_long = stats_second ? n3 : n_s + n3;
-  auto cost = [&](int64_t j) {
-    if (stats_second) return j < n3 ? 1.0 : (j < n3 + n_s ? 1.1 : 0.79);
-    return j < n_s ? 1.1 : (j < n_s + n3 ? 1.0 : 0.79);
-  };
-  const int64_t total = pairs * n_items;
+double plan_makespan(int64_t pairs, int n3, int n2, int n_s, int cus_per_xcd) {
+  const int n_items = n3 + n2;
+  const int64_t total = pairs * n_items, total_s = pairs * n_s;
   const int64_t per = total / 8, rem = total % 8;
   double worst = 0.0;
   std::vector<double> order;
   for (int x = 0; x < 8; ++x) {
     const int64_t start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
     const int64_t end = start + per + (x < rem ? 1 : 0);
-    if (end <= start) continue;
-    order.clear();
-    for (int pass = 0; pass < 2; ++pass)
-      for (int64_t p = start / n_items; p <= (end - 1) / n_items; ++p) {
-        const int64_t j0 = std::max<int64_t>(pass ? n_long : 0, start - p * n_items);
-        const int64_t j1 = std::min<int64_t>(pass ? n_items : n_long, end - p * n_items);
-        for (int64_t j = j0; j < j1; ++j) order.push_back(cost(j));
-      }
+    order.assign(total_s / 8 + (x < total_s % 8 ? 1 : 0), 0.84);
+    if (end > start)
+      for (int pass = 0; pass < 2; ++pass)
+        for (int64_t p = start / n_items; p <= (end - 1) / n_items; ++p) {
+          const int64_t j0 = std::max<int64_t>(pass ? n3 : 0, start - p * n_items);
+          const int64_t j1 = std::min<int64_t>(pass ? n_items : n3, end - p * n_items);
+          for (int64_t j = j0; j < j1; ++j) order.push_back(j < n3 ? 1.0 : 0.79);
+        }
     std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
     for (int c = 0; c < cus_per_xcd; ++c) cu.push(0.0);
     double last = 0.0;
@@ -932,28 +945,25 @@ double plan_makespan(int64_t pairs, int n_s, int n3, int n2, bool stats_second, 
 }
 
 BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int n_s, int cus_per_xcd) {
-  const int left = std::max(0, max_chunk - n_s * qw2);
-  const int n3_max = (left + qw3 - 1) / qw3;
-  BlockPlan best{n3_max, 0, 0};
+  const int n3_max = (std::max(0, max_chunk) + qw3 - 1) / qw3;
+  BlockPlan best{n3_max, 0};
   // Large launches run many rounds, where the last one matters little: keep three-column blocks.
-  if (pairs * (n3_max + n_s) > (1 << 16) || cus_per_xcd <= 0) return best;
+  if (pairs * (n3_max + n_s) > (1 << 16) || cus_per_xcd <= 0 || n3_max == 0) return best;
   static std::mutex mu;
   static std::map<std::tuple<int, int64_t, int, int, int>, BlockPlan> cache;
   const auto key = std::make_tuple(max_chunk, pairs, qw2, n_s, cus_per_xcd);
   std::lock_guard<std::mutex> lock(mu);
   const auto hit = cache.find(key);
   if (hit != cache.end()) return hit->second;
-  double best_t = plan_makespan(pairs, n_s, n3_max, 0, false, cus_per_xcd);
+  double best_t = plan_makespan(pairs, n3_max, 0, n_s, cus_per_xcd);
   // Each three-column block traded for two-column ones adds work (0.79 x 1.5 > 1): a dozen
   // trades fill any last round.
-  for (int n3 = n3_max; n3 >= std::max(0, n3_max - 12); --n3) {
-    const int n2 = (left - n3 * qw3 + qw2 - 1) / qw2;
-    for (int second = 0; second <= (n_s > 0 ? 1 : 0); ++second) {
-      const double t = plan_makespan(pairs, n_s, n3, n2, second != 0, cus_per_xcd);
-      if (t < best_t - 1e-9) {
-        best_t = t;
-        best = BlockPlan{n3, n2, second};
-      }
+  for (int n3 = n3_max - 1; n3 >= std::max(0, n3_max - 12); --n3) {
+    const int n2 = (max_chunk - n3 * qw3 + qw2 - 1) / qw2;
+    const double t = plan_makespan(pairs, n3, n2, n_s, cus_per_xcd);
+    if (t < best_t - 1e-9) {
+      best_t = t;
+      best = BlockPlan{n3, n2};
     }
   }
   if (cache.size() >= 4096) cache.clear();  // a caller cycling through many shapes recomputes
@@ -974,6 +984,41 @@ int cus_per_xcd() {
     cached[dev].store(per, std::memory_order_relaxed);
   }
   return per;
+}
+
+// A stream per device for the statistics kernel, which runs beside the prefill kernel: forked
+// from the caller's stream and joined back into it with two events, under one lock per device so
+// that calls from several host threads do not interleave their fork and join. Created at the
+// device's first call with statistics (a call that is not being captured into a graph), held until
+// the process ends, at the default priority.
+struct SideStream {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+SideStream* side_stream() {
+  static SideStream side[64];
+  static std::mutex init_mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(init_mu);
+  SideStream& ss = side[dev];
+  if (!ss.stream) {
+    hipStream_t st = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      if (f) (void)hipEventDestroy(f);
+      (void)hipStreamDestroy(st);
+      return nullptr;
+    }
+    ss.fork = f;
+    ss.join = j;
+    ss.stream = st;
+  }
+  return &ss;
 }
 
 struct ObsStats {
@@ -1044,26 +1089,46 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
     constexpr int W = UKV_PREFILL_WAVES;
     const int qw2 = W * 2 * (16 / n_rep), qw3 = W * 3 * (16 / n_rep);
     const int64_t pairs = (int64_t)n_groups * batch;
-    // the statistics blocks cover the last obs queries
+    // the statistics blocks cover the last obs queries; the prefill kernel's blocks the rest
     a.n_s = obs ? (a.obs + qw2 - 1) / qw2 : 0;
-    const BlockPlan plan = choose_plan(max_chunk, pairs, qw2, qw3, a.n_s, cus_per_xcd());
+    a.q_skip = a.n_s * qw2;
+    const BlockPlan plan = choose_plan(max_chunk - a.q_skip, pairs, qw2, qw3, a.n_s, cus_per_xcd());
     a.n3 = plan.n3;
     a.n2 = plan.n2;
-    a.stats_second = plan.stats_second;
-    const int64_t wgs = (int64_t)(a.n_s + a.n3 + a.n2) * pairs;
-    if (wgs == 0) return UKV_OK;
-    if (wgs > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
-    const dim3 grid((unsigned)wgs);
-    if (!obs) {
-      if (dtype == UKV_DTYPE_BF16)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), grid, dim3(64 * W), 0, stream, a);
+    const int64_t wgs = (int64_t)(a.n3 + a.n2) * pairs, wgs_s = (int64_t)a.n_s * pairs;
+    if (wgs > INT32_MAX || wgs_s > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
+    auto launch_main = [&](hipStream_t st) {
+      if (dtype == UKV_DTYPE_BF16 && wgs_s)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
+      else if (dtype == UKV_DTYPE_BF16)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
+      else if (wgs_s)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
       else
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), grid, dim3(64 * W), 0, stream, a);
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
+    };
+    auto launch_stats = [&](hipStream_t st) {
+      if (dtype == UKV_DTYPE_BF16)
+        hipLaunchKernelGGL((paged_prefill_stats_kernel<UKV_DTYPE_BF16, W>), dim3((unsigned)wgs_s), dim3(64 * W), 0, st,
+                           a);
+      else
+        hipLaunchKernelGGL((paged_prefill_stats_kernel<UKV_DTYPE_F16, W>), dim3((unsigned)wgs_s), dim3(64 * W), 0, st,
+                           a);
+    };
+    if (wgs_s == 0) {
+      if (wgs > 0) launch_main(stream);
+    } else if (wgs == 0) {
+      launch_stats(stream);
     } else {
-      if (dtype == UKV_DTYPE_BF16)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), grid, dim3(64 * W), 0, stream, a);
-      else
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, true>), grid, dim3(64 * W), 0, stream, a);
+      SideStream* ss = side_stream();
+      if (!ss) return UKV_ERR_LAUNCH;
+      std::lock_guard<std::mutex> lock(ss->mu);
+      if (hipEventRecord(ss->fork, stream) != hipSuccess || hipStreamWaitEvent(ss->stream, ss->fork, 0) != hipSuccess)
+        return UKV_ERR_LAUNCH;
+      launch_stats(ss->stream);
+      if (hipEventRecord(ss->join, ss->stream) != hipSuccess) return UKV_ERR_LAUNCH;
+      launch_main(stream);
+      if (hipStreamWaitEvent(stream, ss->join, 0) != hipSuccess) return UKV_ERR_LAUNCH;
     }
   } else {
     const dim3 grid(total_q, num_q_heads);
