@@ -247,3 +247,45 @@ def test_c_decode_on_compacted_tables(c5, cuda):
         assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), f"layer {layer}: relabelling changed it"
         del k2, v2
     log("decode on compacted tables matches")
+
+
+def test_d_selected_writeback_from_dense_raw_kv_full_size(c5, cuda):
+    """The unchanged scheduler's selected writeback at config 5's shape: two sequences of 32768
+    tokens, each layer's raw K/V dense [8, 32768, 128] (core/scheduler.py:509, 541, 702-733), the
+    top-k of the config's scores per layer, 4 sink + 407 selected + 8 window pages written into
+    FIFO pages of a second pool by ukv_retain_writeback_dense (one launch per sequence), against
+    the oracle's writeback of the same bytes (core/scheduler.py:735-799, 805-878): page ids, free
+    list and every byte of the pool."""
+    k, eff = c5["k"], c5["eff"]
+    keep = c5["keep"]
+    N2 = 2 * keep + 5
+    pool2 = PagedKVPool(16, LAYERS, HKV, D, torch.bfloat16, num_blocks=N2, device=cuda)
+    pool2.k_cache.zero_()
+    pool2.v_cache.zero_()
+    alloc2 = pool_oracle.FifoAllocator(N2)
+    assert pool2.allocate_blocks(3) == alloc2.allocate_blocks(3)  # the FIFO head is not page 0
+    kn = np.zeros((LAYERS, N2, 16, HKV, D), dtype=np.int16)
+    vn = np.zeros_like(kn)
+    sel_np = co.select_topk(c5["scores"], k)
+    sel_dev = compaction.select_blocks(torch.from_numpy(c5["scores"]).to(cuda), k)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(SEED + 23)
+    for b in (0, 5):
+        raw_dev = [(torch.randn((HKV, CTX, D), generator=g, device=cuda).to(torch.bfloat16),
+                    torch.randn((HKV, CTX, D), generator=g, device=cuda).to(torch.bfloat16)) for _ in range(LAYERS)]
+        log(f"selected writeback of sequence {b}: {2 * LAYERS * HKV * CTX * D * 2 / 1e9:.1f} GB of dense raw KV")
+        got = compaction.selected_writeback(pool2, raw_dev, sel_dev[b * LAYERS:(b + 1) * LAYERS], eff, "ratio",
+                                            sink_len=SINK, obs_len=OBS)
+        raw_host = [(K.view(torch.int16).cpu().numpy(), V.view(torch.int16).cpu().numpy()) for K, V in raw_dev]
+        del raw_dev
+        sels = [list(sel_np[b * LAYERS + layer]) for layer in range(LAYERS)]
+        exp = co.selected_writeback(kn, vn, alloc2, raw_host, sels, eff, "ratio", SINK, OBS)
+        del raw_host
+        assert got == exp and len(got) == keep
+        assert pool2.free_blocks == alloc2.free_blocks
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(pool2.k_cache.view(torch.int16).cpu().numpy(), kn)
+    np.testing.assert_array_equal(pool2.v_cache.view(torch.int16).cpu().numpy(), vn)
+    log("selected writeback bit-exact: page ids, free list, every pool byte")
+    del pool2
+    torch.cuda.empty_cache()
