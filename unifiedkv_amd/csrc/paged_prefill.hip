@@ -298,20 +298,22 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       gload16(rv[i], a.v + (uint64_t)pg * (uint32_t)a.v_sp + voff[i]);
     }
   };
-  bool wide_mine = false;  // this thread saw a bf16 V value fp16 cannot hold
+  // The largest bf16 V magnitude this thread stored (as 16-bit patterns), over every tile:
+  // checked once after the loop for values fp16 cannot hold.
+  u16x2 amag = {0, 0};
   auto store = [&](int u, int slot, int id0, int id1, u32x4 (&rk)[ITEMS], u32x4 (&rv)[ITEMS]) {
     const bool full = page_ok(id0) && page_ok(id1) && kTileKeys * (u + 1) <= Lk;
-    u16x2 amag = {0, 0};
     // The other register set's 2 * ITEMS loads were issued after this set's.
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) vm_wait<2 * ITEMS>(rk[i], rv[i]);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const bool ok = full || (page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk);
-      const u32x4 v0 = rv[i];
-      u32x4 v;
+      u32x4 v = rv[i];
+      if (!full) {  // (wave-uniform) rows past the sequence or on an invalid page hold junk
+        const bool ok = page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = ok ? v0[c] : 0u;
+        for (int c = 0; c < 4; ++c) v[c] = ok ? v[c] : 0u;
+      }
       if constexpr (kBf16) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = bf16x2_to_f16x2(v[c], amag);
@@ -319,7 +321,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       *reinterpret_cast<u32x4*>(&k_s[slot][lds_row[i]][8 * lds_ch[i]]) = rk[i];
       *reinterpret_cast<u32x4*>(&v_s[slot][lds_row[i]][8 * lds_ch[i]]) = v;
     }
-    if (kBf16) wide_mine |= __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(amag, u16x2{0x477F, 0x477F})) != 0u;
   };
 
   // Page ids of tiles t .. t+3 (t_id[j] = tile t + j).
@@ -565,6 +566,7 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
+  const bool wide_mine = kBf16 && __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(amag, u16x2{0x477F, 0x477F})) != 0u;
   if (kBf16 && __syncthreads_or(wide_mine)) {
     prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, max(q0, 0), min(C, q0 + qw), wv, WAVES, lane);
     return;
