@@ -348,21 +348,34 @@ def compact_selected(pool, seq_page_lists: Sequence[Sequence[int]], seq_lens: Se
     layers = pool.num_layers
     results: List[List[int]] = []
     eff_lens: List[int] = []
+    # Every selection is range-checked on the device before any sequence is copied, with one
+    # host synchronisation for the whole call (one per sequence would leave the GPU idle between
+    # the launches).
+    sels, checks = [], []
+    for L, sel in zip(seq_lens, selections):
+        selt = None if sel is None else _selection_tensor(sel, layers, dev)
+        sels.append(selt)
+        if selt is not None and selt.shape[1]:
+            n_mid = max(1, -(-(int(L) - sink_len - obs_len) // 16))
+            checks.append(((selt < 0) | (selt >= n_mid)).any())
+        else:
+            checks.append(torch.zeros((), dtype=torch.bool, device=dev))
+    if checks:
+        bad = torch.stack(checks)
+        if bool(bad.any()):
+            s = int(torch.nonzero(bad)[0, 0])
+            raise ValueError(f"compact_selected: sequence {s} selects blocks outside the middle")
     try:
-        for s, (pages, L, sel) in enumerate(zip(seq_page_lists, seq_lens, selections)):
+        for s, (pages, L, selt) in enumerate(zip(seq_page_lists, seq_lens, sels)):
             L = int(L)
             pages = [int(x) for x in pages]
             _check_pool_ids(pool, pages, f"compact_selected: sequence {s}")
             if L > 16 * len(pages) or L < 0:
                 raise ValueError(f"compact_selected: sequence {s} holds {len(pages)} pages for {L} tokens")
-            if sel is None:
-                mode, selt, k = "too_short", None, 0
+            if selt is None:
+                mode, k = "too_short", 0
             else:
-                mode = "ratio"
-                selt = _selection_tensor(sel, layers, dev)
-                k = int(selt.shape[1])
-                if k and bool(((selt < 0) | (selt >= max(1, -(-(L - sink_len - obs_len) // 16)))).any()):
-                    raise ValueError(f"compact_selected: sequence {s} selects blocks outside the middle")
+                mode, k = "ratio", int(selt.shape[1])
             sink, obs, k, dst_len = _retain_map(L, mode, int(sink_len), int(obs_len), k)
             if sink > L:
                 raise ValueError(f"compact_selected: sequence {s} is shorter than its sink")
