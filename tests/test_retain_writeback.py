@@ -416,6 +416,27 @@ def test_compact_selected_rejects_out_of_range_selections(cuda):
 
 
 @pytest.mark.gpu
+def test_compact_selected_refuses_before_taking_pages(cuda):
+    """A later sequence's invalid input is refused before the earlier ones are copied: the free list
+    and the pool bytes stay as they were."""
+    rng = np.random.default_rng(2)
+    pool, kn, vn = _dev_pool(cuda, 2, 80, 2, 64, rng)
+    a, b = pool.allocate_blocks(20), pool.allocate_blocks(10)
+    before = pool.free_blocks
+    good = torch.tensor([[0, 3], [1, 2]], dtype=torch.int32, device=cuda)
+    for lens, sels, what in (([300, 161], [good, None], "holds 10 pages"),  # 161 tokens in 10 pages
+                             ([300, 8], [good, good], "shorter than its sink"),
+                             ([300, 150], [good, torch.tensor([[0, 99], [1, 2]], dtype=torch.int32, device=cuda)],
+                              "outside the middle")):
+        with pytest.raises(ValueError, match=what):
+            compaction.compact_selected(pool, [a, b], lens, sels, sink_len=16, obs_len=16)
+        assert pool.free_blocks == before
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(pool.k_cache.view(torch.int16).cpu().numpy(), kn)
+    np.testing.assert_array_equal(pool.v_cache.view(torch.int16).cpu().numpy(), vn)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("old_len,kept", [(16 * 8 + 5, [0, 2, 3, 7, 8]), (16 * 9, [1, 4, 8]), (100, [0, 6, 9, 12])])
 def test_prune_window_matches_oracle(cuda, old_len, kept):
     rng = np.random.default_rng(old_len)

@@ -343,42 +343,41 @@ def compact_selected(pool, seq_page_lists: Sequence[Sequence[int]], seq_lens: Se
     FIFO in sequence order; with free_sources each sequence's old pages are freed, in list
     order, right after its copy (core/offload.py:1262). On MemoryError the sequences finished
     before stay compacted (``err.partial``) unless free_sources is False, in which case every
-    page taken by this call is returned."""
+    page taken by this call is returned. Invalid input (a page outside the pool, a length beyond
+    its pages or below its sink, a selection outside the middle) raises ValueError before any
+    page is taken."""
     dev = pool.device
     layers = pool.num_layers
     results: List[List[int]] = []
     eff_lens: List[int] = []
-    # Every selection is range-checked on the device before any sequence is copied, with one
-    # host synchronisation for the whole call (one per sequence would leave the GPU idle between
-    # the launches).
-    sels, checks = [], []
-    for L, sel in zip(seq_lens, selections):
+    # Every input is checked before any page is taken, so that a refusal leaves the pool as it
+    # was; the selections are range-checked on the device with one host synchronisation for the
+    # whole call (one per sequence would leave the GPU idle between the launches).
+    plan, checks = [], []
+    for s, (pages, L, sel) in enumerate(zip(seq_page_lists, seq_lens, selections)):
+        L = int(L)
+        pages = [int(x) for x in pages]
+        _check_pool_ids(pool, pages, f"compact_selected: sequence {s}")
+        if L > 16 * len(pages) or L < 0:
+            raise ValueError(f"compact_selected: sequence {s} holds {len(pages)} pages for {L} tokens")
         selt = None if sel is None else _selection_tensor(sel, layers, dev)
-        sels.append(selt)
-        if selt is not None and selt.shape[1]:
-            n_mid = max(1, -(-(int(L) - sink_len - obs_len) // 16))
+        mode, k = ("too_short", 0) if selt is None else ("ratio", int(selt.shape[1]))
+        sink, obs, k, dst_len = _retain_map(L, mode, int(sink_len), int(obs_len), k)
+        if sink > L:
+            raise ValueError(f"compact_selected: sequence {s} is shorter than its sink")
+        if selt is not None and k:
+            n_mid = max(1, -(-(L - sink_len - obs_len) // 16))
             checks.append(((selt < 0) | (selt >= n_mid)).any())
         else:
             checks.append(torch.zeros((), dtype=torch.bool, device=dev))
+        plan.append((pages, L, selt, sink, obs, k, dst_len))
     if checks:
         bad = torch.stack(checks)
         if bool(bad.any()):
             s = int(torch.nonzero(bad)[0, 0])
             raise ValueError(f"compact_selected: sequence {s} selects blocks outside the middle")
     try:
-        for s, (pages, L, selt) in enumerate(zip(seq_page_lists, seq_lens, sels)):
-            L = int(L)
-            pages = [int(x) for x in pages]
-            _check_pool_ids(pool, pages, f"compact_selected: sequence {s}")
-            if L > 16 * len(pages) or L < 0:
-                raise ValueError(f"compact_selected: sequence {s} holds {len(pages)} pages for {L} tokens")
-            if selt is None:
-                mode, k = "too_short", 0
-            else:
-                mode, k = "ratio", int(selt.shape[1])
-            sink, obs, k, dst_len = _retain_map(L, mode, int(sink_len), int(obs_len), k)
-            if sink > L:
-                raise ValueError(f"compact_selected: sequence {s} is shorter than its sink")
+        for s, (pages, L, selt, sink, obs, k, dst_len) in enumerate(plan):
             n_req = int(math.ceil(max(1, dst_len) / int(pool.B)))
             ids = pool.allocate_blocks(n_req)
             if len(ids) != n_req:
