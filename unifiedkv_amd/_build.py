@@ -40,6 +40,13 @@ HIPCC_FLAGS = [
     "-munsafe-fp-atomics",
 ]
 
+# Per-source additions. The prefill tile loop is issue-bound and its speed follows the
+# instruction schedule: LLVM's iterative-ILP machine scheduler ran it 1.5 % faster than the
+# default one on config 4 (max-ILP 2.7 % and max-memory-clause 0.5 % slower), outputs bit-identical.
+SOURCE_FLAGS = {
+    "paged_prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -58,7 +65,7 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         objs.append(obj)
-        cmd = [cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
