@@ -83,10 +83,12 @@ def build() -> Path:
 
 
 def _load():
+    """Load liboracle.so. Never builds it: the callers (tests, bench.py) may already hold a GPU
+    context, and a fork + exec of make from such a process is not allowed; build() does it ahead."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
-            build()
+            raise RuntimeError(f"{LIB_PATH} is missing: build it first (__graft_entry__.build() or make -C oracle)")
         lib = ctypes.CDLL(str(LIB_PATH))
         P = ctypes.c_void_p
         I = ctypes.c_int

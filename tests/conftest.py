@@ -10,6 +10,12 @@ if str(ROOT) not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; runs the HIP kernels")
+    # The oracle's C library is built here, before anything in this process touches a GPU; the
+    # oracle's loader itself never builds (tests may hold a GPU context by then).
+    if not (ROOT / "oracle" / "liboracle.so").exists():
+        import subprocess
+
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
 
 
 def gpu_available() -> bool:

@@ -61,11 +61,21 @@ def test_pool_sizing_formula(monkeypatch):
 
     monkeypatch.setattr(torch.cuda, "get_device_properties", lambda dev=None: Props())
     monkeypatch.setattr(torch.cuda, "memory_allocated", lambda dev=None: 16 * 1024**3)
-    for frac in (0.2, 0.75):
+    # Known answers of core/pool.py:36-45 worked by hand: 288 GiB total, 16 GiB in use, a 10 %
+    # reserve of 28.8 GiB leaves 243.2 GiB; one block of 32 layers x 16 tokens x 8 heads x 128
+    # x 2 B x (K, V) is 2 MiB, i.e. 512 blocks per GiB: 243.2 * 512 * frac blocks, floored.
+    # frac 0.2 -> 24903.68 -> 24903; frac 0.75 -> 93388.8 -> 93388.
+    for frac, n_total in ((0.2, 24903), (0.75, 93388)):
         pool = PagedKVPool(16, 32, 8, 128, torch.float16, frac, 48.0)
-        assert pool.N_total == pool_oracle.pool_size(288 * 1024**3, 16 * 1024**3, frac, 32, 16, 8, 128)
+        assert pool.N_total == n_total
+        assert pool_oracle.pool_size(288 * 1024**3, 16 * 1024**3, frac, 32, 16, 8, 128) == n_total
+        assert (pool.N_wm_low, pool.N_wm_high) == (int(0.15 * n_total), int(0.40 * n_total))
         assert pool.cpu_budget == int(48.0 * 1024**3) and pool.cpu_used_bytes == 0
         assert not pool.is_allocated
+    # Less free memory than one block still yields one block (the max(1, .) of :45).
+    monkeypatch.setattr(torch.cuda, "memory_allocated", lambda dev=None: 288 * 1024**3 - 2 * 1024**2)
+    assert PagedKVPool(16, 32, 8, 128, torch.float16, 0.75, 48.0).N_total == 1
+    assert pool_oracle.pool_size(288 * 1024**3, 288 * 1024**3 - 2 * 1024**2, 0.75, 32, 16, 8, 128) == 1
 
 
 @pytest.mark.parametrize("lens", [[3, 0, 7], [1], [2048] * 4, [5, 128, 33]])

@@ -113,6 +113,36 @@ def test_oracle_matches_torch_sdpa_with_a_bottom_right_causal_mask():
                                    rtol=1e-5, atol=1e-6)
 
 
+def _logical_kv(case, b):
+    """Sequence b's keys and values [L, H_kv, D] (fp32) in logical order, from the written pool."""
+    k, v = written_pool(case)
+    f = lambda a: oracle.bits_to_f32(a, workloads.DTYPE_CODES[case["dtype"]])
+    L = int(case["kv_lens"][b])
+    pages = case["block_table"][b][: (L + 15) // 16]
+    Hkv, D = k.shape[2], k.shape[3]
+    return f(k)[pages].reshape(-1, Hkv, D)[:L], f(v)[pages].reshape(-1, Hkv, D)[:L]
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 2), (8, 1)])
+@pytest.mark.parametrize("prefix", [0, 37])
+def test_prefill_rows_f32_matches_the_fp64_oracle(Hq, Hkv, prefix):
+    """The config-4 CPU baseline's formulation (dense fp32 matmul-softmax-matmul of sampled chunk
+    rows) equals the pinned fp64 prefill at n_rep 1, 4 and 8, with and without a prefix."""
+    chunk = 23
+    case = make_case(40 + Hq + Hkv + prefix, [prefix], [chunk], Hq=Hq, Hkv=Hkv, D=32)
+    exp = expected(case)
+    K, V = _logical_kv(case, 0)
+    f = lambda a: oracle.bits_to_f32(a, oracle.DT_BF16)
+    rows = np.array([0, 5, chunk - 1])
+    got = prefill_oracle.prefill_rows_f32(f(case["q"])[rows], K, V, prefix + rows, softmax_scale=case["scale"],
+                                          n_rep=Hq // Hkv)
+    np.testing.assert_allclose(got, exp[rows], rtol=1e-5, atol=1e-5)
+    # A causal mask one key too wide is caught at this tolerance.
+    wide = prefill_oracle.prefill_rows_f32(f(case["q"])[rows[:2]], K, V, prefix + rows[:2] + 1,
+                                           softmax_scale=case["scale"], n_rep=Hq // Hkv)
+    assert np.abs(wide - exp[rows[:2]]).max() > 1e-3
+
+
 # ---------------------------------------------------------------------- GPU
 def to_dev(case, cuda):
     import torch
@@ -250,6 +280,73 @@ def test_prefill_last_row_matches_page16_decode(cuda):
     dec = page16_decode_attention(t["q"][last].contiguous(), t["k_cache"], t["v_cache"], t["block_table"],
                                   t["kv_lens"], softmax_scale=case["scale"], n_rep=4)
     check(out[last].float().cpu().numpy(), dec.float().cpu().numpy(), "prefill last row vs decode")
+
+
+def test_max_chunk_is_derived_or_checked_on_the_host():
+    """As core/varlen.py:28-29 derives max_seqlen from the lengths: with host lengths an
+    understated max_chunk is refused before any launch, and a missing one is derived."""
+    import torch
+
+    from unifiedkv_amd import prefill
+
+    assert prefill._max_chunk([0, 5, 12, 12], None) == 7
+    assert prefill._max_chunk(torch.tensor([0, 5, 12], dtype=torch.int32), 9) == 9
+    assert prefill._max_chunk([0, 5, 12], 7) == 7
+    assert prefill._max_chunk(None, 3, chunk_lens=[3, 1]) == 3
+    for cu, mc, lens in (([0, 5, 12], 6, None), (torch.tensor([0, 5, 12]), 6, None), (None, 2, [3, 1]),
+                         ([0, 1], -1, None)):
+        with pytest.raises(RuntimeError, match="paged_prefill_shape_unsupported:max_chunk"):
+            prefill._max_chunk(cu, mc, chunk_lens=lens)
+    # through the public entry point, on CPU tensors: refused in the host checks, before the library
+    z = lambda *s: torch.zeros(s, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="max_chunk"):
+        prefill.chunked_prefill(z(12, 4, 128), z(12, 1, 128), z(12, 1, 128), z(4, 16, 1, 128), z(4, 16, 1, 128),
+                                torch.zeros((2, 2), dtype=torch.int32), [0, 5, 12], [5, 7], softmax_scale=0.1,
+                                n_rep=4, max_chunk=6)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["tiled", "scalar", "stats"])
+def test_understated_max_chunk_on_device_lengths_gives_nan_rows(cuda, path):
+    """Lengths only on the device cannot be checked without a synchronisation: a chunk longer than
+    the declared max_chunk comes out NaN in every row of its output (loud), not as stale memory;
+    chunks within it are unaffected. "stats" is the call that also writes SnapKV row statistics
+    (through the C entry point: the Python wrapper reads those lengths back to check the window);
+    the over-long chunk's statistics rows are NaN and flagged for the scorer to recompute."""
+    import torch
+
+    from unifiedkv_amd import _ext, prefill, snapkv
+
+    D = 128 if path != "scalar" else 64
+    case = make_case(61, [300, 40, 10], [150, 90, 20], Hq=8, Hkv=2, D=D)
+    mc = 100  # sequence 0's chunk (150 queries) is longer
+    t = to_dev(case, cuda)
+    prefill.write_chunk_kv(t["k_cache"], t["v_cache"], t["k_new"], t["v_new"], t["block_table"], t["cu"], t["kv_lens"],
+                           max(case["chunk"]))
+    st = snapkv.ObsStats(3, 1, 8, sink_len=16, obs_len=16, softmax_scale=case["scale"], device=cuda)
+    exp = expected(case, n_rep=4)
+    for _ in range(2):  # the second call's output memory held the first call's values
+        if path != "stats":
+            out = prefill.paged_prefill_attention(t["q"], t["k_cache"], t["v_cache"], t["block_table"], t["cu"],
+                                                  t["kv_lens"], softmax_scale=case["scale"], n_rep=4, max_chunk=mc)
+        else:
+            out = torch.empty_like(t["q"])
+            code = _ext.load().ukv_paged_prefill_obs_stats(
+                t["q"].data_ptr(), t["k_cache"].data_ptr(), t["v_cache"].data_ptr(), t["block_table"].data_ptr(),
+                t["cu"].data_ptr(), t["kv_lens"].data_ptr(), out.data_ptr(), 3, int(t["q"].shape[0]), mc, 8, 2, D, 4,
+                int(t["block_table"].shape[1]), int(t["k_cache"].shape[0]), _ext.i64_array(t["q"].stride()[:2]),
+                _ext.i64_array(t["k_cache"].stride()[:3]), _ext.i64_array(t["v_cache"].stride()[:3]),
+                float(case["scale"]), _ext.UKV_DTYPE_BF16, 16, 16, *st.layer_view(0),
+                torch.cuda.current_stream().cuda_stream)
+            assert code == _ext.UKV_OK
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        assert np.isnan(got[:150]).all(), f"{path}: rows of the over-long chunk must all be NaN"
+        check(got[150:], exp[150:], f"{path}: chunks within max_chunk")
+    if path == "stats":
+        rows = st.data[0, 0].cpu().numpy()  # sequence 0, layer 0: [H_q, obs, 2]
+        assert np.isnan(rows[..., 0]).all() and (rows[..., 1] == 1).all()
+        assert np.isfinite(st.data[1:, 0, ..., 0].cpu().numpy()).all()
 
 
 @pytest.mark.gpu

@@ -104,6 +104,35 @@ def test_dominant_key_marks_its_block_and_pooled_neighbours():
     assert np.all(got[3:6] > 0.999) and np.all(np.delete(got, [3, 4, 5]) < 1e-3)
 
 
+@pytest.mark.parametrize("n_rep,obs,L", [(1, 8, 16 + 70 + 8), (4, 16, 16 + 96 + 16), (2, 5, 16 + 33 + 5)])
+def test_score_heads_f32_matches_the_fp64_steps(n_rep, obs, L):
+    """The scores CPU baseline's fp32 formulation, per KV group, equals the per-key head maximum of
+    the fp64 steps: weights rebuilt from the pinned row normalisers (obs_row_stats), averaged over
+    the queries and maximised over the group's heads; block sums and maxpool3 of the maximum over
+    groups then give score_layer_blocks."""
+    rng = np.random.default_rng(obs + L)
+    H_kv, D, sink = 2, 16, 16
+    K = rng.standard_normal((H_kv, L, D)).astype(np.float32)
+    Q = rng.standard_normal((H_kv * n_rep, obs, D)).astype(np.float32) * 2
+    scale = D ** -0.5
+    K_mid, N = so.mid_keys(K.astype(np.float64), sink, obs, 16)
+    lse2 = so.obs_row_stats(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep, scale=scale)  # [H_q, obs]
+    per_group = []
+    for g in range(H_kv):
+        heads = slice(g * n_rep, (g + 1) * n_rep)
+        got = so.score_heads_f32(K_mid[g].astype(np.float32), Q[heads], scale)
+        s2 = np.matmul(Q[heads].astype(np.float64), K_mid[g].T) * scale / math.log(2.0)
+        exp = np.exp2(s2 - lse2[heads][..., None]).mean(axis=1).max(axis=0)
+        assert got.shape == (N * 16,)
+        np.testing.assert_allclose(got, exp, rtol=0, atol=1e-6 * exp.max())
+        per_group.append(got.astype(np.float64))
+    s = np.max(per_group, axis=0)
+    blocks = s.reshape(N, 16).sum(axis=-1)
+    pooled = so.maxpool3(blocks) if N >= 3 else blocks
+    ref = so.score_layer_blocks(K, Q, sink_len=sink, obs_len=obs, n_rep=n_rep, scale=scale)
+    np.testing.assert_allclose(pooled, ref, rtol=1e-5, atol=0)
+
+
 def test_too_short_and_block_counts_of_the_reference_tests():
     K = np.zeros((1, 16 + 16 + 15, 4))
     assert so.score_layer_blocks(K, np.zeros((1, 16, 4)), sink_len=16, obs_len=16, n_rep=1).size == 0

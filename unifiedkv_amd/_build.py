@@ -6,10 +6,12 @@ The shared library lands next to this file so that it travels with the tree.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
 from pathlib import Path
+from typing import Dict, List
 
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
@@ -40,12 +42,59 @@ HIPCC_FLAGS = [
     "-munsafe-fp-atomics",
 ]
 
-# Per-source additions. The prefill tile loop is issue-bound and its speed follows the
-# instruction schedule: LLVM's iterative-ILP machine scheduler ran it 1.5 % faster than the
-# default one on config 4 (max-ILP 2.7 % and max-memory-clause 0.5 % slower), outputs bit-identical.
-SOURCE_FLAGS = {
-    "paged_prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
-}
+# Per-source additions. (LLVM's iterative-ILP machine scheduler ran the prefill tile loop 1.5 %
+# faster, but left the bf16 instance at 255 VGPRs with 20 B/lane of scratch for SGPR spills,
+# which the resource guard below refuses.)
+SOURCE_FLAGS: Dict[str, List[str]] = {}
+
+
+# Resource guard. These kernels issue global loads by inline asm (global_load_dwordx4) and wait
+# for them with a hand-placed s_waitcnt vmcnt(N): the compiler sees the destination registers as
+# written when the asm statement retires, while the data lands later. A VGPR spill or any
+# scratch traffic could store, copy or reload such a register while its load is in flight, so
+# every instance must compile with ScratchSize 0 and no spilled VGPRs. (SGPRs spilled into the
+# lanes of a VGPR the compiler reserves for that purpose touch no load destination and no
+# memory; once no such lane is left they go through scratch, which ScratchSize reports.)
+GUARDED_SOURCES = ("page16_decode.hip", "paged_prefill.hip", "snapkv_score.hip")
+GUARDED_KERNELS = ("page16_split_kernel", "paged_prefill_kernel", "paged_prefill_stats_kernel", "snap_tile_kernel")
+REMARK_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+_FN_RE = re.compile(r"remark: Function Name: (\S+)")
+_FIELD_RE = re.compile(r"remark:\s+(.+?): (\S+) \[-Rpass-analysis=kernel-resource-usage\]")
+
+
+def parse_resource_usage(text: str) -> Dict[str, Dict[str, str]]:
+    """The compiler's kernel-resource-usage remarks -> {mangled kernel name: {field: value}}."""
+    out: Dict[str, Dict[str, str]] = {}
+    cur = None
+    for ln in text.splitlines():
+        m = _FN_RE.search(ln)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = _FIELD_RE.search(ln)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = m.group(2)
+    return out
+
+
+def guarded(name: str) -> bool:
+    """True for a mangled name of one of GUARDED_KERNELS (the Itanium length-prefixed identifier)."""
+    return any(f"{len(k)}{k}I" in name or f"{len(k)}{k}E" in name for k in GUARDED_KERNELS)
+
+
+def resource_violations(usage: Dict[str, Dict[str, str]]) -> List[str]:
+    bad = []
+    for name, f in usage.items():
+        if not guarded(name):
+            continue
+        scratch = f.get("ScratchSize [bytes/lane]")
+        vspill = f.get("VGPRs Spill")
+        if scratch is None or vspill is None:
+            bad.append(f"{name}: resource-usage remark incomplete ({f})")
+        elif int(scratch) != 0 or int(vspill) != 0:
+            bad.append(f"{name}: ScratchSize {scratch} B/lane, VGPRs spilled {vspill}")
+    return bad
 
 
 def hipcc() -> str:
@@ -65,7 +114,9 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         objs.append(obj)
-        cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+        remarks = [REMARK_FLAG] if src in GUARDED_SOURCES else []
+        cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *remarks, f"-I{INCLUDE}", "-c", str(CSRC / src),
+               "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
@@ -90,8 +141,33 @@ def _drain(procs):
         lines = [ln for ln in out.splitlines() if "packed-fp32-ops" not in ln]
         if p.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src}:\n" + "\n".join(lines))
+        if src in GUARDED_SOURCES:
+            usage = parse_resource_usage(out)
+            if not any(guarded(n) for n in usage):
+                raise RuntimeError(f"{src}: no resource-usage remarks for the guarded kernels")
+            bad = resource_violations(usage)
+            if bad:
+                raise RuntimeError(f"{src}: kernels with hand-issued loads must not spill or use scratch:\n  "
+                                   + "\n  ".join(bad))
+            lines = [ln for ln in lines if "kernel-resource-usage" not in ln and not _is_remark_context(ln)]
         if lines:
             print("\n".join(lines), file=sys.stderr)
+
+
+def _is_remark_context(ln: str) -> bool:
+    """The source excerpt clang prints under each remark (a line number gutter and a caret line)."""
+    return bool(re.match(r"^\s*\d+ \|", ln) or re.match(r"^\s*\|\s*\^", ln))
+
+
+def guarded_resource_usage(src: str, jobs_flags=()) -> Dict[str, Dict[str, str]]:
+    """Compile one guarded source for the device only (no object kept) and return its remarks."""
+    cc = hipcc()
+    cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *jobs_flags, REMARK_FLAG, "--cuda-device-only",
+           f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", os.devnull]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout[-4000:]}")
+    return parse_resource_usage(res.stdout)
 
 
 if __name__ == "__main__":

@@ -268,17 +268,23 @@ def selected_writeback(pool, raw_by_layer: Sequence[Tuple[torch.Tensor, torch.Te
     effective_len and mode as _compute_per_layer_selected_blocks returns them. Allocates
     ceil(max(1, effective_len) / B) pages FIFO and returns them (every layer's new block map);
     when the allocation fails MemoryError is raised, and when the write is refused the pages are
-    freed again before the error propagates, as the reference's transaction does."""
+    freed again before the error propagates, as the reference's transaction does. A selection
+    entry outside the middle blocks (a -1 pad of select_blocks, an index past the middle) raises
+    ValueError before any page is taken (one host synchronisation for a device selection)."""
     if len(raw_by_layer) != pool.num_layers:
         raise RuntimeError(f"selected_writeback_missing_raw layers={len(raw_by_layer)}")
+    L = int(raw_by_layer[0][0].shape[1])
+    sel = _selection_tensor(selected_mid_blocks_by_layer, pool.num_layers, pool.device) \
+        if mode not in ("input_le_budget", "too_short") else None
+    if sel is not None and sel.numel():
+        n_mid = max(1, -(-(L - int(sink_len) - int(obs_len)) // 16))
+        if bool(((sel < 0) | (sel >= n_mid)).any()):
+            raise ValueError("selected_writeback: a selection entry lies outside the middle blocks")
     n_req = int(math.ceil(max(1, int(effective_len)) / int(pool.B)))
     block_ids = pool.allocate_blocks(n_req)
     if not block_ids:
         raise MemoryError(f"Cannot allocate {n_req} blocks")
     try:
-        L = int(raw_by_layer[0][0].shape[1])
-        sel = _selection_tensor(selected_mid_blocks_by_layer, pool.num_layers, pool.device) \
-            if mode not in ("input_le_budget", "too_short") else None
         k = int(sel.shape[1]) if sel is not None else 0
         sink, obs, k, dst_len = _retain_map(L, mode, int(sink_len), int(obs_len), k)
         if dst_len != int(effective_len):

@@ -79,6 +79,9 @@ struct PrefillArgs {
   // statistics (obs > 0), the last q_skip = n_s * (two-column block) queries of each chunk are the
   // n_s blocks of the statistics kernel, launched beside it.
   int n3, n2, q_skip, n_s;
+  // The longest chunk the caller declared: the block plan covers that many queries. A chunk
+  // longer than it gets NaN in every row of its output (its K/V were not all written either).
+  int max_chunk;
   float scale, scale_log2;
   // SnapKV observation statistics (obs > 0): the query blocks that hold a sequence's last obs
   // queries run in the statistics kernel, which also writes, for each of those queries and q head
@@ -592,6 +595,21 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   }
 }
 
+// Rows lo .. hi - 1 of sequence b's chunk, the q heads of KV group g, set to NaN (0x7FFF is a
+// NaN in fp16 and in bf16). For chunks longer than the declared max_chunk: the block plan does not
+// reach their first queries and the chunk write stopped at max_chunk tokens, so every block of
+// such a chunk writes NaN into its rows instead of attending, the lowest block also into the rows
+// below it.
+template <int WAVES>
+__device__ void prefill_nan_rows(const PrefillArgs& a, int b, int g, int lo, int hi) {
+  const int h0 = g * a.n_rep;
+  const int per = min(a.n_rep, a.Hq - h0) * a.D;  // a query row's heads of the group, contiguous
+  const int64_t n = (int64_t)max(0, hi - lo) * per;
+  uint16_t* base = a.out + ((int64_t)(a.cu_q[b] + lo) * a.Hq + h0) * a.D;
+  for (int64_t i = threadIdx.x; i < n; i += 64 * WAVES)
+    base[(i / per) * a.Hq * a.D + i % per] = 0x7FFFu;
+}
+
 // The s-th work item an XCD dispatches from its range [start, end) of pair-major item numbers
 // (item j of pair p is number p * n + j): first the items j < nl of the range's pairs, pair by
 // pair, then the items j >= nl. Returns false past the range.
@@ -650,9 +668,16 @@ paged_prefill_kernel(const PrefillArgs a) {
   xcd_range(n_items * a.n_groups * a.B, blockIdx.x & 7, start, end);
   if (!locate_item(start, end, n_items, a.n3, blockIdx.x >> 3, pair, j)) return;  // (never: the grid holds total)
   const int g = pair % a.n_groups, b = pair / a.n_groups;
-  const int top = a.cu_q[b + 1] - a.cu_q[b] - (SKIP ? a.q_skip : 0);  // the blocks end here
+  const int C = a.cu_q[b + 1] - a.cu_q[b];
+  const int top = C - (SKIP ? a.q_skip : 0);  // the blocks end here
   const int qpb = 16 / a.n_rep;
   const int qw2 = WAVES * 2 * qpb, qw3 = WAVES * 3 * qpb;
+  if (C > a.max_chunk) {
+    const int q0 = j < a.n3 ? top - qw3 * (j + 1) : top - qw3 * a.n3 - qw2 * (j - a.n3 + 1);
+    const int q1 = min(C, j < a.n3 ? q0 + qw3 : q0 + qw2);
+    prefill_nan_rows<WAVES>(a, b, g, j == n_items - 1 ? 0 : max(0, q0), q1);
+    return;
+  }
   if (j < a.n3)
     prefill_tile<DT, WAVES, false, 3>(a, b, g, top - qw3 * (j + 1), lds);
   else
@@ -677,7 +702,18 @@ paged_prefill_stats_kernel(const PrefillArgs a) {
   const int g = pair % a.n_groups, b = pair / a.n_groups;
   const int C = a.cu_q[b + 1] - a.cu_q[b];
   const int qw2 = WAVES * 2 * (16 / a.n_rep);
-  prefill_tile<DT, WAVES, true, 2>(a, b, g, C - qw2 * (js + 1), lds);
+  const int q0 = C - qw2 * (js + 1);
+  if (C > a.max_chunk) {  // (see prefill_nan_rows); the rows' statistics are flagged for the scorer
+    const bool lowest = js == a.n_s - 1 && a.n3 + a.n2 == 0;
+    prefill_nan_rows<WAVES>(a, b, g, lowest ? 0 : max(0, q0), min(C, q0 + qw2));
+    for (int i = threadIdx.x; i < a.n_rep * qw2; i += 64 * WAVES) {
+      const int qi = q0 + i / a.n_rep, h = g * a.n_rep + i % a.n_rep;
+      if (qi >= max(0, C - a.obs) && qi < C && h < a.Hq)
+        a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)h * a.obs + (qi - (C - a.obs))] = make_float2(NAN, 1.f);
+    }
+    return;
+  }
+  prefill_tile<DT, WAVES, true, 2>(a, b, g, q0, lds);
 }
 
 // Marks every observation row of the call as recomputed-by-the-scorer: (0, 1) at row
@@ -701,6 +737,10 @@ __global__ void __launch_bounds__(256) paged_prefill_scalar_kernel(const Prefill
   const int C = a.cu_q[b + 1] - a.cu_q[b];
   const int i = row - a.cu_q[b];
   if (i < 0 || i >= C) return;
+  if (C > a.max_chunk) {  // longer than declared: its K/V were not all written (see prefill_nan_rows)
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) a.out[((int64_t)row * a.Hq + h) * a.D + d] = 0x7FFFu;
+    return;
+  }
   const int Lk = kv_len_of(a, b);
   const int L = max(0, min(Lk, Lk - C + i + 1));
   const int g = h / a.n_rep;
@@ -1042,6 +1082,8 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
   if (n_groups > num_kv_heads) return UKV_ERR_GQA;
   if (total_q < 0 || max_chunk < 0 || max_blocks < 0 || num_pages < 0) return UKV_ERR_INVALID_ARGUMENT;
   if (total_q == 0) return UKV_OK;
+  // The chunks hold total_q queries, so the longest holds at least total_q / batch of them.
+  if ((int64_t)max_chunk * batch < total_q) return UKV_ERR_INVALID_ARGUMENT;
   if (!q || !out || !cu_seqlens_q || !kv_lens || !q_strides || !k_strides || !v_strides)
     return UKV_ERR_INVALID_ARGUMENT;
   if (max_blocks > 0 && (!block_table || !k_cache || !v_cache || num_pages <= 0)) return UKV_ERR_INVALID_ARGUMENT;
@@ -1068,6 +1110,7 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
   a.D = head_dim;
   a.max_blocks = max_blocks;
   a.num_pages = num_pages;
+  a.max_chunk = max_chunk;
   a.scale = softmax_scale;
   a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);

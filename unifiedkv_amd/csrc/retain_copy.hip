@@ -155,6 +155,10 @@ int launch_retain(RetainArgs a, int layers, const void* const* k_layers, const v
   if (2 * slices > 65535) return UKV_ERR_INVALID_ARGUMENT;
   if (!a.dst_ids) return UKV_ERR_INVALID_ARGUMENT;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Every layer's dense K/V pointer is checked before the first launch: a refusal writes nothing.
+  if (!a.paged)
+    for (int i = 0; i < layers; ++i)
+      if (!k_layers[i] || !v_layers[i] || !al16(k_layers[i]) || !al16(v_layers[i])) return UKV_ERR_INVALID_ARGUMENT;
   const int per = a.paged ? 65535 : kRetainLayersPerLaunch;
   for (int l0 = 0; l0 < layers; l0 += per) {
     RetainArgs b = a;
@@ -164,8 +168,6 @@ int launch_retain(RetainArgs a, int layers, const void* const* k_layers, const v
       for (int i = 0; i < nl; ++i) {
         b.src[0][i] = static_cast<const uint16_t*>(k_layers[l0 + i]);
         b.src[1][i] = static_cast<const uint16_t*>(v_layers[l0 + i]);
-        if (!b.src[0][i] || !b.src[1][i] || !al16(b.src[0][i]) || !al16(b.src[1][i]))
-          return UKV_ERR_INVALID_ARGUMENT;
       }
     }
     hipLaunchKernelGGL(retain_copy_kernel, dim3(16 * pages, nl, 2 * slices), dim3(kRetainThreads), 0, s, b);

@@ -96,23 +96,24 @@ def _workspace_bytes(dev_index, batch, num_q_heads, head_dim, max_blocks) -> int
         return max(int(_ext.load().ukv_page16_workspace_bytes(batch, num_q_heads, head_dim, max_blocks)), 256)
 
 
-# One workspace per (device, stream), reused by every call on that stream (calls on one stream
-# are ordered; the workspace needs no initialisation, include/ukv.h). A workspace outgrown by a
-# larger shape is replaced and the old one kept alive, since a captured graph may still use it.
-# Under graph capture a missing or small workspace is allocated for that call alone (it then
-# belongs to the graph's memory pool), never cached.
+# One workspace per (device, stream), reused by every eager call on that stream (calls on one
+# stream are ordered; the workspace needs no initialisation, include/ukv.h). A workspace outgrown
+# by a larger shape is replaced and the old one kept alive for the calls still queued on it.
+# Under graph capture every call gets a workspace of its own from the graph's memory pool, never
+# the cached one: a graph may be replayed on another stream, beside eager calls or other graphs
+# captured on the same stream, and a shared buffer would race there.
 _WORKSPACES = {}
 _RETIRED = []
 
 
 def _workspace(batch, num_q_heads, head_dim, max_blocks, dev, stream) -> torch.Tensor:
     need = _workspace_bytes(dev.index, batch, num_q_heads, head_dim, max_blocks)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(need, dtype=torch.uint8, device=dev)
     key = (dev.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is not None and ws.numel() >= need:
         return ws
-    if torch.cuda.is_current_stream_capturing():
-        return torch.empty(need, dtype=torch.uint8, device=dev)
     fresh = torch.empty(need if ws is None else max(need, 2 * ws.numel()), dtype=torch.uint8, device=dev)
     if ws is not None:
         _RETIRED.append(ws)

@@ -88,11 +88,11 @@ class PagedKVPool:
         self.N_wm_low = max(1, int(0.15 * self.N_total))
         self.N_wm_high = max(2, int(0.40 * self.N_total))
 
-        self._table_lists: Optional[List[List[int]]] = None
-        self._table_dev: Optional[torch.Tensor] = None
-        # The last id list token I/O uploaded: callers pass the same list once per layer.
-        self._ids_list: Optional[List[int]] = None
-        self._ids_dev: Optional[torch.Tensor] = None
+        # The last block table uploaded (page lists, stream, device table).
+        self._table_cache: Optional[Tuple[List[List[int]], int, torch.Tensor]] = None
+        # The last id list token I/O uploaded (list, stream, device ids): callers pass the same
+        # list once per layer.
+        self._ids_cache: Optional[Tuple[List[int], int, torch.Tensor]] = None
 
     # ------------------------------------------------------------------ storage
     @property
@@ -125,10 +125,8 @@ class PagedKVPool:
             return False
         self._k_cache = None
         self._v_cache = None
-        self._table_lists = None
-        self._table_dev = None
-        self._ids_list = None
-        self._ids_dev = None
+        self._table_cache = None
+        self._ids_cache = None
         if torch.cuda.is_available():
             torch.cuda.empty_cache()
         return True
@@ -185,13 +183,17 @@ class PagedKVPool:
         return X
 
     def _device_ids(self, block_ids) -> torch.Tensor:
-        """int32 device copy of block_ids, reused while the caller passes an equal list (the exact
-        list compare costs ~1 % of a pinned upload)."""
+        """int32 device copy of block_ids, reused while the caller passes an equal list on the same
+        stream (the exact list compare costs ~1 % of a pinned upload). The copy is ordered on the
+        stream it was uploaded on, so a call on another stream uploads its own; list, stream and
+        tensor are kept as one tuple, so a concurrent caller never pairs one list with another's ids."""
         ids = [int(x) for x in block_ids] if not isinstance(block_ids, list) else block_ids
-        if self._ids_dev is not None and self._ids_list == ids:
-            return self._ids_dev
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        cached = self._ids_cache
+        if cached is not None and cached[1] == stream and cached[0] == ids:
+            return cached[2]
         dev = torch.tensor(ids, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
-        self._ids_list, self._ids_dev = list(ids), dev
+        self._ids_cache = (list(ids), stream, dev)
         return dev
 
     def write_kv_to_blocks(self, layer_id: int, block_ids: List[int], K: torch.Tensor, V: torch.Tensor):
@@ -220,14 +222,17 @@ class PagedKVPool:
 
     # ------------------------------------------------------------- block tables
     def block_table_for(self, seq_block_ids_list: Sequence[Sequence[int]]) -> torch.Tensor:
-        """Zero-padded int32 [batch, max_len] device table; one pinned H2D copy, reused while unchanged."""
+        """Zero-padded int32 [batch, max_len] device table; one pinned H2D copy, reused while unchanged
+        and asked for on the stream it was uploaded on (the copy is ordered on that stream only)."""
         cacheable = isinstance(seq_block_ids_list, list) and all(isinstance(x, list) for x in seq_block_ids_list)
-        if cacheable and self._table_dev is not None and self._table_lists == seq_block_ids_list:
-            return self._table_dev
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        cached = self._table_cache
+        if cacheable and cached is not None and cached[1] == stream and cached[0] == seq_block_ids_list:
+            return cached[2]
         host = pack_block_table(seq_block_ids_list)
         table = torch.from_numpy(host).pin_memory().to(self.device, non_blocking=True)
-        self._table_lists = [list(ids) for ids in seq_block_ids_list] if cacheable else None
-        self._table_dev = table if cacheable else None
+        # list, stream and table as one tuple: a concurrent caller never pairs one with another's
+        self._table_cache = ([list(ids) for ids in seq_block_ids_list], stream, table) if cacheable else None
         return table
 
     def build_block_table(self, layer_id: int, seq_block_ids_list: List[List[int]]

@@ -26,11 +26,33 @@ def _i32(t, dev):
     return t.to(device=dev, dtype=torch.int32).contiguous()
 
 
-def _max_chunk(cu_seqlens_q, max_chunk):
-    if max_chunk is not None:
-        return int(max_chunk)
-    cu = cu_seqlens_q.tolist() if torch.is_tensor(cu_seqlens_q) else list(cu_seqlens_q)  # host sync if on device
-    return max((cu[i + 1] - cu[i] for i in range(len(cu) - 1)), default=0)
+def _chunk_lens_on_host(cu_seqlens_q):
+    """The chunk lengths when ``cu_seqlens_q`` lives on the host (a sequence or a CPU tensor), else None."""
+    if torch.is_tensor(cu_seqlens_q):
+        if cu_seqlens_q.device.type != "cpu":
+            return None
+        cu = cu_seqlens_q.tolist()
+    else:
+        cu = [int(x) for x in cu_seqlens_q]
+    return [cu[i + 1] - cu[i] for i in range(len(cu) - 1)]
+
+
+def _max_chunk(cu_seqlens_q, max_chunk, chunk_lens=None):
+    """The longest chunk: derived from the lengths when no ``max_chunk`` is given (as
+    core/varlen.py:28-29 derives max_seqlen; a device synchronisation when ``cu_seqlens_q`` is on
+    the device), checked against them when they are on the host. A ``max_chunk`` given with
+    device-only lengths is trusted; a chunk longer than it comes out as NaN rows."""
+    if chunk_lens is None:
+        chunk_lens = _chunk_lens_on_host(cu_seqlens_q)
+    if max_chunk is None:
+        if chunk_lens is None:
+            cu = cu_seqlens_q.tolist()  # host sync
+            chunk_lens = [cu[i + 1] - cu[i] for i in range(len(cu) - 1)]
+        return max(chunk_lens, default=0)
+    mc = int(max_chunk)
+    if mc < 0 or (chunk_lens is not None and mc < max(chunk_lens, default=0)):
+        raise RuntimeError("paged_prefill_shape_unsupported:max_chunk")
+    return mc
 
 
 def write_chunk_kv(k_layer: torch.Tensor, v_layer: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
@@ -110,9 +132,10 @@ def paged_prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
         if any(c < obs_stats.obs_len for c in chunk_lens):
             raise RuntimeError("paged_prefill_shape_unsupported:obs_window_spans_chunks")
         stats_view = obs_stats.layer_view(layer_id)
+        host_lens = (chunk_lens, seq_lens)
     if dev.type != "cuda" or any(t.device != dev for t in (k_cache, v_cache, bt, cu, lens)):
         raise RuntimeError("paged_prefill_unavailable:device")
-    mc = _max_chunk(cu_seqlens_q, max_chunk)
+    mc = _max_chunk(cu_seqlens_q, max_chunk, None if host_lens is None else host_lens[0])
     out = torch.empty((total_q, Hq, D), dtype=q.dtype, device=dev)
     args = [q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), cu.data_ptr(), lens.data_ptr(),
             out.data_ptr(), B, total_q, mc, Hq, Hkv, D, int(n_rep), int(bt.shape[1]),
