@@ -26,8 +26,9 @@ Other BASELINE configs (parity cases, measured on request; one JSON line each):
                                rotating through the 32 layers
   --workload step              a 32-layer decode step on the config-2 batch: prologue, then per
                                layer the append kernel and the decode, beside the fused
-                               append/decode and the reference's call pattern (step_ragged:
-                               the config-3 batch)
+                               append/decode, both with the per-layer calls replayed from a HIP
+                               graph, and the reference's call pattern (step_ragged: the config-3
+                               batch; step_5c: config 5c's shape, B=8 at L=6704)
   --workload offload_seq       config 5b's volume through the per-sequence offload / prefetch entry
                                points over the pinned page arena, beside the reference's per-page pattern
   --workload prefill_pages     config 4's sequences prefilled in 2048-token chunks over 32 layers with
@@ -309,31 +310,53 @@ def run_decode(args, dev):
 
 
 # ------------------------------------------------------------------- 32-layer decode step
+def layout_5c(rng, B: int = 8, pages: int = 419, spare: int = 1024):
+    """Config 5c's decode shape without the compaction in front of it: B = 8 sequences of
+    L = 6704 tokens (419 pages), H_q 32 / H_kv 8 / D 128 bf16, tables drawn from a random
+    permutation of the pool (as the compacted tables are: FIFO pages of a churned pool)."""
+    import numpy as np
+
+    from unifiedkv_amd import workloads
+
+    N = B * pages + spare
+    perm = rng.permutation(N)[: B * pages].astype(np.int32)
+    return dict(B=B, Hq=32, Hkv=8, D=128, dtype="bf16", N=N, seqlens=np.full(B, 16 * pages, dtype=np.int32),
+                block_table=workloads.tables_from_pages([perm[i * pages:(i + 1) * pages] for i in range(B)]))
+
+
+STEP_LAYOUTS = {"step": "config2_longctx", "step_ragged": "config3_ragged", "step_5c": "config5c_shape"}
+
+
 def run_step(args, dev):
-    """One decode step of a 32-layer model over the config-2 (or config-3) batch: the step's
-    prologue (new pages + attention lengths, once) and per layer the append kernel and the
-    decode (DecodeBatch's default). Beside it, on the same pool and batch and interleaved with
-    it: the append fused into the decode kernel (DecodeBatch(fused_append=True)), and the
-    reference's call pattern (core/scheduler.py:1092-1160, 401-418: per-row table uploads per
-    layer, torch index_put of the token, attn_lens = old + 1) with this build's decode kernel,
-    so the difference is the prologue's."""
+    """One decode step of a 32-layer model over the config-2 batch (step_ragged: config 3's,
+    step_5c: config 5c's shape): the step's prologue (new pages + attention lengths, once) and
+    per layer the append kernel and the decode (DecodeBatch's default). Beside it, on the same
+    pool and batch and interleaved with it: the append fused into the decode kernel
+    (DecodeBatch(fused_append=True)); both again with the 32 per-layer calls captured in a HIP
+    graph (one per parity of the step, replayed after the eager prologue); and the reference's
+    call pattern (core/scheduler.py:1092-1160, 401-418: per-row table uploads per layer, torch
+    index_put of the token, attn_lens = old + 1) with this build's decode kernel, so the
+    difference is the prologue's."""
     import numpy as np
     import torch
 
-    from unifiedkv_amd import page16_native, page_ops, workloads
+    from unifiedkv_amd import page16_native, workloads
     from unifiedkv_amd.decode_step import DecodeBatch
     from unifiedkv_amd.pool import PagedKVPool
 
     n_layers = 32
     rng = np.random.default_rng(args.seed)
-    ragged = args.workload == "step_ragged"
-    layout = workloads.layout_ragged(rng) if ragged else workloads.layout_longctx(rng)
+    name = STEP_LAYOUTS[args.workload]
+    layout = {"step": workloads.layout_longctx, "step_ragged": workloads.layout_ragged,
+              "step_5c": layout_5c}[args.workload](rng)
     B, Hq, Hkv, D = layout["B"], layout["Hq"], layout["Hkv"], layout["D"]
     lens0 = [int(x) for x in layout["seqlens"]]
     lists0 = [[int(x) for x in layout["block_table"][b, : (L + 15) // 16]] for b, L in enumerate(lens0)]
-    # Room for the pages the timed steps add (one per sequence per 16 steps, three variants).
-    total_steps = 3 * (args.warmup + 2 * args.steps)
+    # Room for the pages the timed steps add (one per sequence per 16 steps, five variants).
+    half = max(1, args.steps // 2)
+    total_steps = 4 * (args.warmup + 2 * half + 4) + max(3, args.steps // 4) + args.warmup
     N = int(layout["N"]) + B * (total_steps // 16 + 2)
+    cap = max(len(x) for x in lists0) + total_steps // 16 + 2  # device tables never grow while timed
     pool = PagedKVPool(16, n_layers, Hkv, D, torch.bfloat16, num_blocks=N, device=dev)
     used = set(x for ids in lists0 for x in ids)
     pool.allocate_blocks(N)
@@ -347,37 +370,73 @@ def run_step(args, dev):
     kns = [torch.randn((B, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_layers)]
     vns = [torch.randn((B, Hkv, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(n_layers)]
     scale, n_rep = D ** -0.5, Hq // Hkv
-    log(f"[bench] step: {n_layers} layers, pool {N} pages/layer "
+    log(f"[bench] step ({name}): {n_layers} layers, pool {N} pages/layer "
         f"({2 * pool.k_cache.numel() * 2 / 2**30:.1f} GiB)")
 
     # (a) DecodeBatch's default: prologue + per layer append kernel and decode;
-    # (b) the same with the append fused into the decode kernel (opt-in). Timed interleaved.
-    batches = {"append_then_decode": DecodeBatch(pool, [list(x) for x in lists0], lens0),
-               "fused_append": DecodeBatch(pool, [list(x) for x in lists0], lens0, fused_append=True)}
+    # (b) the same with the append fused into the decode kernel (opt-in);
+    # (c), (d) both with the per-layer calls replayed from HIP graphs. Timed interleaved.
+    batches = {"append_then_decode": DecodeBatch(pool, [list(x) for x in lists0], lens0, capacity_blocks=cap),
+               "fused_append": DecodeBatch(pool, [list(x) for x in lists0], lens0, capacity_blocks=cap,
+                                           fused_append=True)}
     lens_log = []
+
+    def layers(batch):
+        for l in range(n_layers):
+            batch.attention(l, qs[l], kns[l], vns[l], softmax_scale=scale, n_rep=n_rep)
 
     def make_step(batch):
         def step():
             lens_log.append(batch.seq_lens)
             batch.begin_step()
-            for l in range(n_layers):
-                batch.attention(l, qs[l], kns[l], vns[l], softmax_scale=scale, n_rep=n_rep)
+            layers(batch)
             batch.end_step()
         return step
 
-    times = {k: [] for k in batches}
-    half = max(1, args.steps // 2)
+    graphs = {}
+    for key, batch in batches.items():
+        for _ in range(2):  # one eager step per parity first (workspaces, tables in place)
+            make_step(batch)()
+        torch.cuda.synchronize()
+        per_parity = {}
+        for _ in range(2):
+            batch.begin_step()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                layers(batch)
+            gr.replay()  # capture records only: this replay is the step's work
+            per_parity[batch.step_parity] = gr
+            batch.end_step()
+        graphs[key] = per_parity
+    torch.cuda.synchronize()
+
+    def make_graph_step(key):
+        batch, per_parity = batches[key], graphs[key]
+
+        def step():
+            lens_log.append(batch.seq_lens)
+            batch.begin_step()
+            per_parity[batch.step_parity].replay()
+            batch.end_step()
+        return step
+
+    variants = {"append_then_decode": make_step(batches["append_then_decode"]),
+                "fused_append": make_step(batches["fused_append"]),
+                "graph_append_then_decode": make_graph_step("append_then_decode"),
+                "graph_fused_append": make_graph_step("fused_append")}
+    times = {k: [] for k in variants}
+    order = list(variants)
     for rnd in range(2):
-        for name in (("append_then_decode", "fused_append") if rnd == 0 else ("fused_append", "append_then_decode")):
-            ms, _ = event_time_ms(make_step(batches[name]), half, args.warmup if rnd == 0 else 1)
-            times[name].append(ms)
-    default_ms = sum(times["append_then_decode"]) / 2
-    fused_ms = sum(times["fused_append"]) / 2
+        for key in (order if rnd == 0 else order[::-1]):
+            ms, _ = event_time_ms(variants[key], half, args.warmup if rnd == 0 else 1)
+            times[key].append(ms)
+    us = {k: sum(v) / len(v) * 1e3 for k, v in times.items()}
+    default_ms = us["append_then_decode"] * 1e-3
     mean_len = float(np.mean([np.mean(x) for x in lens_log])) + 1.0
-    log(f"[bench] step append-then-decode: {default_ms * 1e3:.1f} us, fused append: {fused_ms * 1e3:.1f} us")
+    log("[bench] step " + ", ".join(f"{k}: {v:.1f} us" for k, v in us.items()))
     fused = batches["fused_append"]
 
-    # (c) the reference's call pattern with this build's decode kernel
+    # (e) the reference's call pattern with this build's decode kernel
     ref_lists = [list(x) for x in lists0]
     ref_lens = list(lens0)
 
@@ -410,8 +469,10 @@ def run_step(args, dev):
     max_blocks = int(fused.block_table.shape[1])
     layer_bytes = workloads.decode_bytes(np.full(B, mean_len), B, Hq, Hkv, D, max_blocks) + 2 * B * Hkv * D * 2
     step_bytes = n_layers * layer_bytes
+    best = min(us, key=us.get)
+    best_ms = us[best] * 1e-3
     gbps = step_bytes / (default_ms * 1e-3) / 1e9
-    name = "config3_ragged" if ragged else "config2_longctx"
+    gbps_best = step_bytes / (best_ms * 1e-3) / 1e9
     return {
         "metric": f"Decode step over 32 layers (prologue + append + decode per layer), {name}, tokens/s",
         "value": round(B / (default_ms * 1e-3), 1),
@@ -428,12 +489,16 @@ def run_step(args, dev):
         "config": {"workload": f"decode_step_32_layers_{name}", "layers": n_layers, "batch": B,
                    "start_lengths_mean": float(np.mean(lens0)), "num_q_heads": Hq, "num_kv_heads": Hkv,
                    "head_dim": D, "page_size": 16, "pool_pages_per_layer": N},
-        "us_per_step": {"append_then_decode": round(default_ms * 1e3, 1), "fused_append": round(fused_ms * 1e3, 1),
-                        "reference_call_pattern": round(ref_ms * 1e3, 1)},
+        "us_per_step": {**{k: round(v, 1) for k, v in us.items()}, "reference_call_pattern": round(ref_ms * 1e3, 1)},
+        "us_per_layer": {k: round(v / n_layers, 2) for k, v in us.items()},
+        "layer_bytes": int(layer_bytes),
+        "fastest": {"variant": best, "us_per_layer": round(us[best] / n_layers, 2), "gbps": round(gbps_best, 1),
+                    "frac": round(gbps_best / PEAK_HBM_GBPS, 4)},
         "us_per_layer_saved_vs_reference_pattern": round((ref_ms - default_ms) * 1e3 / n_layers, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                     "note": "whole step: 32 x (KV pages read + token rows written) / step time"},
+                     "note": "whole step (DecodeBatch default, eager): 32 x (KV pages read + token rows written) "
+                             "/ step time"},
         "cpu_baseline": None,
     }
 
@@ -1143,7 +1208,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "ragged", "tiny", "compaction", "offload", "compacted_decode", "prefill",
-                             "step", "step_ragged", "scores", "offload_seq", "prefill_pages"])
+                             "step", "step_ragged", "step_5c", "scores", "offload_seq", "prefill_pages"])
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (known bytes) for scaling PMC counters")
     args = ap.parse_args()
@@ -1186,7 +1251,7 @@ def main():
         rec = run_offload(args, dev)
     elif args.workload == "prefill":
         rec = run_prefill(args, dev)
-    elif args.workload in ("step", "step_ragged"):
+    elif args.workload in STEP_LAYOUTS:
         rec = run_step(args, dev)
     elif args.workload == "scores":
         rec = run_scores(args, dev)

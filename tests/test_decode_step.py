@@ -407,3 +407,64 @@ def test_layer_calls_replay_from_a_captured_graph(cuda, fused_append):
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), eager[1].view(torch.int16))
     batch.end_step()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused_append", [False, True])
+def test_per_parity_graphs_replay_a_run_of_steps(cuda, fused_append):
+    # One graph of the per-layer calls per parity of the step (the attention lengths alternate
+    # between two device buffers), replayed after each step's eager prologue for 20 steps that
+    # cross page boundaries and take new pages: every step's outputs and, at the end, every pool
+    # byte, the page lists and the free list equal an eager run of the same steps on a twin pool.
+    from unifiedkv_amd.decode_step import DecodeBatch
+
+    rng = np.random.default_rng(33)
+    n_layers, Hq, Hkv, D, N, dtype = 3, 32, 8, 128, 96, "bf16"
+    lens0 = [40, 16, 100, 5, 31]
+    B = len(lens0)
+    kc = _dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda)
+    vc = _dev(_rand_bits(rng, (n_layers, N, 16, Hkv, D), dtype), dtype, cuda)
+    pools, batches = [], []
+    for _ in range(2):
+        pool = PagedKVPool(16, n_layers, Hkv, D, _tdt(dtype), num_blocks=N, device=cuda)
+        pool.k_cache.copy_(kc)
+        pool.v_cache.copy_(vc)
+        lists = [pool.allocate_blocks(max(1, -(-L // 16))) for L in lens0]
+        pools.append(pool)
+        batches.append(DecodeBatch(pool, lists, lens0, capacity_blocks=16, fused_append=fused_append))
+    eager_b, graph_b = batches
+    scale = 1.0 / math.sqrt(D)
+    steps = 20
+    ins = [[tuple(_dev(_rand_bits(rng, s, dtype), dtype, cuda) for s in ((B, Hq, D), (B, Hkv, D), (B, Hkv, D)))
+            for _ in range(n_layers)] for _ in range(steps)]
+    # static inputs the graphs read; each step's inputs are copied in before its replay
+    static = [tuple(t.clone() for t in ins[0][layer]) for layer in range(n_layers)]
+
+    def run_layers(batch, src):
+        return [batch.attention(layer, *src[layer], softmax_scale=scale, n_rep=Hq // Hkv) for layer in range(n_layers)]
+
+    graphs, outs = {}, {}
+    for step in range(steps):
+        eager_b.begin_step()
+        exp = [o.clone() for o in run_layers(eager_b, ins[step])]
+        eager_b.end_step()
+        for layer in range(n_layers):
+            for dst, src in zip(static[layer], ins[step][layer]):
+                dst.copy_(src)
+        graph_b.begin_step()
+        par = graph_b.step_parity
+        if par not in graphs:
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                outs[par] = run_layers(graph_b, static)
+            graphs[par] = gr
+        graphs[par].replay()
+        graph_b.end_step()
+        torch.cuda.synchronize()
+        for layer in range(n_layers):
+            assert torch.equal(outs[par][layer].view(torch.int16), exp[layer].view(torch.int16)), (step, layer)
+    assert graph_b.page_lists == eager_b.page_lists and graph_b.seq_lens == eager_b.seq_lens
+    assert pools[0].free_blocks == pools[1].free_blocks
+    assert torch.equal(pools[0].k_cache.view(torch.int16), pools[1].k_cache.view(torch.int16))
+    assert torch.equal(pools[0].v_cache.view(torch.int16), pools[1].v_cache.view(torch.int16))

@@ -315,11 +315,13 @@ def test_selected_writeback_refusals_free_their_pages(cuda):
         compaction.selected_writeback(pool, dev, [1, -2], 16 + 32 + 16, "ratio", sink_len=16, obs_len=16)
     # device selections (select_blocks' form): a -1 pad or an index past the 17 middle blocks of
     # L = 300 (sink 16, window 16) is refused on the device before any page is taken
+    order = pool.free_blocks
     for bad in ([[1, -1], [2, 3]], [[1, 2], [3, 17]]):
         sel = torch.tensor(bad, dtype=torch.int32, device=cuda)
         with pytest.raises(ValueError, match="outside the middle blocks"):
             compaction.selected_writeback(pool, dev, sel, 16 + 32 + 16, "ratio", sink_len=16, obs_len=16)
-    assert pool.free_blocks == before
+    assert pool.free_blocks == order
+    assert sorted(pool.free_blocks) == sorted(before)
     with pytest.raises(MemoryError):
         compaction.selected_writeback(pool, dev, [], 61 * 16, "too_short", sink_len=16, obs_len=16)
     _assert_pool(pool, kn, vn)

@@ -151,6 +151,13 @@ class DecodeBatch:
         return self._lens_dev[self._cur ^ 1]
 
     @property
+    def step_parity(self) -> int:
+        """0 or 1: which of the two device length buffers holds the lengths before this step. The
+        per-layer calls of an open step read the table, those lengths and the other buffer's; a
+        HIP graph captured from them replays correctly at steps of the same parity."""
+        return self._cur
+
+    @property
     def seq_lens(self) -> List[int]:
         return list(self._lens)
 
