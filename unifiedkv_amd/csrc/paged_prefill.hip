@@ -353,35 +353,41 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 
   auto compute = [&](int t, int slot) {
     const int key0 = t * kTileKeys;
-    // S^T[key][column] for the tile's two 16-key blocks and both column blocks.
-    f32x4 sacc[2][CB];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[slot][kb * 16 + i16][32 * s + 8 * kg]);
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = mfma16x16x32<DT>(ka, qv[cb][s], sacc[kb][cb]);
-      }
-    }
     const bool pg0 = page_ok(t_id[0][0]), pg1 = page_ok(t_id[0][1]);
     const bool full = pg0 && pg1 && key0 + kTileKeys <= Lk && key0 + kTileKeys - 1 <= wpos_min;
-    if (!full) {
-      // key kb*16 + 4kg + r is visible to a column iff it is below lim[kb]
+    // S^T[key][column] for the tile's two 16-key blocks and every column block, masked. (As one
+    // inlined function the register allocator keeps the three-column loop within 256 VGPRs with
+    // no scratch under the iterative-ILP schedule this file is built with; written out in line,
+    // that schedule needed 20 bytes per lane of scratch.)
+    auto scores = [&](f32x4 (&sacc)[2][CB]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int qi = qi0 + cb * qpb;
-        const bool live = qi >= 0 && qi < C && head < a.Hq;
-        const int vis = live ? min(Lk, P0 + qi + 1) - key0 - 4 * kg : -1;  // an unused column sees no key
-        const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis - 16 : 0;
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sacc[kb][cb][r] = r < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
+        for (int s = 0; s < STEPS; ++s) {
+          const u32x4 ka = *reinterpret_cast<const u32x4*>(&k_s[slot][kb * 16 + i16][32 * s + 8 * kg]);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) sacc[kb][cb] = mfma16x16x32<DT>(ka, qv[cb][s], sacc[kb][cb]);
+        }
       }
-    }
+      if (!full) {
+        // key kb*16 + 4kg + r is visible to a column iff it is below lim[kb]
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int qi = qi0 + cb * qpb;
+          const bool live = qi >= 0 && qi < C && head < a.Hq;
+          const int vis = live ? min(Lk, P0 + qi + 1) - key0 - 4 * kg : -1;  // an unused column sees no key
+          const int lim0 = pg0 ? vis : 0, lim1 = pg1 ? vis - 16 : 0;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sacc[kb][cb][r] = r < (kb ? lim1 : lim0) ? sacc[kb][cb][r] : -INFINITY;
+        }
+      }
+    };
+    f32x4 sacc[2][CB];
+    scores(sacc);
     // Softmax: p = 2^(s*scale*log2e - m) as fp16 against the running max m
     // (log2 units) of its column. m moves only when some p of the tile reaches
     // 2^8: the packed fp16 P is checked (non-negative fp16 bit patterns order
