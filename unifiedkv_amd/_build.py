@@ -42,12 +42,14 @@ HIPCC_FLAGS = [
     "-munsafe-fp-atomics",
 ]
 
-# Per-source additions. The prefill tile loop is issue-bound and its speed follows the
-# instruction schedule: LLVM's iterative-ILP machine scheduler runs config 4 4.6 % faster than the
-# default one, outputs bit-identical (max-ILP and max-memory-clause measured slower). The resource
+# Per-source additions. The prefill tile loop and the SnapKV score passes are issue-bound and
+# their speed follows the instruction schedule: LLVM's iterative-ILP machine scheduler runs config
+# 4's prefill 4.6 % and config 5's two-pass scores 1.0 % faster than the default one, outputs
+# bit-identical (max-ILP, max-memory-clause and iterative-minreg measured slower). The resource
 # guard below checks that the schedule leaves no scratch and no spilled VGPRs.
 SOURCE_FLAGS: Dict[str, List[str]] = {
     "paged_prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "snapkv_score.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
 
