@@ -352,11 +352,19 @@ def run_step(args, dev):
     B, Hq, Hkv, D = layout["B"], layout["Hq"], layout["Hkv"], layout["D"]
     lens0 = [int(x) for x in layout["seqlens"]]
     lists0 = [[int(x) for x in layout["block_table"][b, : (L + 15) // 16]] for b, L in enumerate(lens0)]
-    # Room for the pages the timed steps add (one per sequence per 16 steps, five variants).
+    # Room for the pages the steps add: every page consumer (the two DecodeBatches and the
+    # reference pattern) takes up to one page per sequence per 16 of its steps, plus one.
+    # event_time_ms(fn, steps, warmup) calls fn warmup + 2 * steps times.
     half = max(1, args.steps // 2)
-    total_steps = 4 * (args.warmup + 2 * half + 4) + max(3, args.steps // 4) + args.warmup
-    N = int(layout["N"]) + B * (total_steps // 16 + 2)
-    cap = max(len(x) for x in lists0) + total_steps // 16 + 2  # device tables never grow while timed
+    ref_steps = max(3, args.steps // 4)
+    ref_warmup = max(1, args.warmup // 4)
+    # per batch: 2 eager steps and 2 capture steps, then its eager and graph variants, each timed in
+    # two rounds (warm-up W, then 1)
+    batch_steps = 4 + 2 * ((args.warmup + 2 * half) + (1 + 2 * half))
+    ref_calls = ref_warmup + 2 * ref_steps
+    demand = 2 * (batch_steps // 16 + 2) + ref_calls // 16 + 2
+    N = int(layout["N"]) + B * demand
+    cap = max(len(x) for x in lists0) + batch_steps // 16 + 2  # device tables never grow while timed
     pool = PagedKVPool(16, n_layers, Hkv, D, torch.bfloat16, num_blocks=N, device=dev)
     used = set(x for ids in lists0 for x in ids)
     pool.allocate_blocks(N)
@@ -443,7 +451,12 @@ def run_step(args, dev):
     def step_reference_pattern():
         for i, L in enumerate(ref_lens):  # reserve_decode_slot (core/offload.py:838-866)
             if L % 16 == 0:
-                ref_lists[i].extend(pool.allocate_blocks(1))
+                ids = pool.allocate_blocks(1)
+                if not ids:  # the reference raises here too (direct_decode_expand_*_failed)
+                    raise RuntimeError("page16_native_blocked:direct_decode_expand_evict_failed")
+                ref_lists[i].extend(ids)
+            if L // 16 >= len(ref_lists[i]):  # the token's page must be in the table before any launch
+                raise RuntimeError(f"step reference pattern: sequence {i} has no page for position {L}")
         cache_seqlens = torch.tensor(ref_lens, dtype=torch.int32, device=dev)
         width = max(len(ids) for ids in ref_lists)
         for l in range(n_layers):
@@ -462,7 +475,6 @@ def run_step(args, dev):
         for i in range(B):  # commit (core/scheduler.py:1247-1265)
             ref_lens[i] += 1
 
-    ref_steps = max(3, args.steps // 4)
     ref_ms, _ = event_time_ms(step_reference_pattern, ref_steps, max(1, args.warmup // 4))
     log(f"[bench] step reference pattern: {ref_ms * 1e3:.1f} us")
 

@@ -288,7 +288,9 @@ int ukv_select_topk(const float* scores, int64_t row_stride, const int32_t* row_
  * (C_b rows) and kv_lens[b] keys after the chunk, row cu_seqlens_q[b] + i of k_new / v_new
  * ([total, num_heads, head_dim], strides new_strides = {row, head}) goes to position
  * P_b + i = kv_lens[b] - C_b + i: page block_table[b, pos / 16], slot pos % 16. Positions outside
- * [0, 16*max_blocks) and page ids outside [0, num_pages) are skipped.
+ * [0, 16*max_blocks) and page ids outside [0, num_pages) are skipped. max_chunk bounds C_b: rows
+ * i >= max_chunk of a longer chunk are not written (ukv_paged_prefill with the same max_chunk then
+ * returns NaN rows for that sequence).
  */
 int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const int64_t* k_strides, const int64_t* v_strides,
                         const void* k_new, const void* v_new, const int64_t* new_strides, const int32_t* block_table,
@@ -304,7 +306,12 @@ int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const int64_t* k
  *   q    [total_q, num_q_heads, head_dim], element strides q_strides = {row, head}
  *   k/v  [num_pages, 16, num_kv_heads, head_dim], strides {page, token, head}
  *   out  [total_q, num_q_heads, head_dim] contiguous, q's dtype
- * fp32 softmax and accumulation; a row with no visible key yields NaN. max_chunk bounds C_b.
+ * fp32 softmax and accumulation; a row with no visible key yields NaN. max_chunk bounds C_b (the
+ * flash-attn max_seqlen_q, core/varlen.py:28-29, which the Python wrapper derives from or checks
+ * against host lengths): the block plan covers max_chunk queries per sequence, and every row of a
+ * sequence whose C_b exceeds it is written as NaN (its chunk K/V were not all written either), so an
+ * understated max_chunk on device-only lengths is loud, never stale memory. max_chunk * batch
+ * below total_q (necessarily understated) is UKV_ERR_INVALID_ARGUMENT before any launch.
  * Replaces the dense chunked prefill of core/engine.py:1826-1854 (HF attention over the past
  * KV) and core/varlen.py:19-42 (flash_attn_varlen_func, causal=True).
  */
