@@ -27,6 +27,7 @@ import numpy as np
 import torch
 
 from . import page_ops
+from .page16_native import _current_stream
 
 
 def pack_block_table(seq_block_ids_list: Sequence[Sequence[int]]) -> np.ndarray:
@@ -188,7 +189,7 @@ class PagedKVPool:
         stream it was uploaded on, so a call on another stream uploads its own; list, stream and
         tensor are kept as one tuple, so a concurrent caller never pairs one list with another's ids."""
         ids = [int(x) for x in block_ids] if not isinstance(block_ids, list) else block_ids
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _current_stream(self.device)
         cached = self._ids_cache
         if cached is not None and cached[1] == stream and cached[0] == ids:
             return cached[2]
@@ -225,7 +226,7 @@ class PagedKVPool:
         """Zero-padded int32 [batch, max_len] device table; one pinned H2D copy, reused while unchanged
         and asked for on the stream it was uploaded on (the copy is ordered on that stream only)."""
         cacheable = isinstance(seq_block_ids_list, list) and all(isinstance(x, list) for x in seq_block_ids_list)
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = _current_stream(self.device)
         cached = self._table_cache
         if cacheable and cached is not None and cached[1] == stream and cached[0] == seq_block_ids_list:
             return cached[2]
