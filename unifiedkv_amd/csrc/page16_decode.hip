@@ -7,10 +7,11 @@
 //
 // Work decomposition (split-K / flash-decoding):
 //   * grid (G workgroups, 1, kv-group blocks), G = one per CU. The batch's
-//     pages, sequence after sequence, form one list of P pages; workgroup w
+//     pages, sequence after sequence, form one list of P pages; share w
 //     streams pages [w*P/G, (w+1)*P/G) - equal work for every workgroup however
 //     ragged the lengths - crossing sequence boundaries as needed and leaving
-//     one (m, l, acc) partial per sequence segment. One wave per KV head (up to
+//     one (m, l, acc) partial per sequence segment; each XCD runs a contiguous
+//     run of shares. One wave per KV head (up to
 //     eight per workgroup), so a workgroup reads each 32 KiB K page and V page
 //     whole, and every KV byte is read exactly once for all n_rep q heads that
 //     share it (GQA packing).
@@ -217,8 +218,13 @@ __global__ void __launch_bounds__(64 * UKV_PAGE16_WAVES, UKV_PAGE16_MIN_WAVES_PE
   const int wv = threadIdx.x >> 6;
   const int g = blockIdx.z * (blockDim.x >> 6) + wv;
   if (g >= a.n_groups) return;  // whole wave leaves; no workgroup barrier below
-  const int w = blockIdx.x;
   const int G = a.grid_wgs;
+  // Share w of the page list runs on workgroup blockIdx.x = 8 * (w % (G/8)) + w / (G/8): dispatch
+  // puts workgroup i on XCD i % 8, so XCD x runs the contiguous shares x*G/8 .. (x+1)*G/8 - 1 and
+  // the shares that carry one page more than the average (their positions follow P/G) spread evenly
+  // over the XCDs instead of gathering on a few of them. Which workgroup runs a share does not
+  // change its pages, slot or result.
+  const int w = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
   const bool writer = blockIdx.x == 0 && blockIdx.z == 0 && wv == 0;
 
   // The batch's pages in sequence order form one list of P pages; workgroup w
