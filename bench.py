@@ -624,15 +624,36 @@ def run_offload(args, dev):
     stager = PageStager(pool, chunk_pages=512)
     nbytes = 2 * L * n * pool.B * pool.num_kv_heads * pool.head_dim * 2
     log(f"[bench] config 5b: {n} evicted pages per layer, {nbytes / 1e9:.2f} GB each way")
-    # plain pinned copies of the staging chunk's size class: the link's measured peak, the fastest of
-    # eight 1 GiB copies per direction (each timed alone with events)
-    probe = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    probe_h = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
-    _, d2h_runs = event_time_ms(lambda: probe_h.copy_(probe, non_blocking=True), LINK_PROBES, 1)
-    _, h2d_runs = event_time_ms(lambda: probe.copy_(probe_h, non_blocking=True), LINK_PROBES, 1)
-    peak_d2h = (1 << 30) / (min(d2h_runs) * 1e-3) / 1e9
-    peak_h2d = (1 << 30) / (min(h2d_runs) * 1e-3) / 1e9
-    del probe, probe_h
+    # Plain pinned copies, no gather: the link's measured peak per direction is the fastest of
+    # eight runs (each timed alone with events) of two forms, one 1 GiB copy and four 512 MiB
+    # copies back to back (the size of the stager's per-chunk K and V copies, whose per-copy
+    # overhead overlaps the next copy the same way), each on the default stream and on the stager's
+    # own stream, before and after the stager's runs.
+    def probe_link():
+        probe = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        probe_h = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+        half = 1 << 29
+
+        def chunked(dst, src):
+            for _ in range(2):
+                dst[:half].copy_(src[:half], non_blocking=True)
+                dst[half:].copy_(src[half:], non_blocking=True)
+
+        rates = {}
+        for where, st in (("default_stream", torch.cuda.current_stream(dev)), ("stager_stream", stager.stream)):
+            with torch.cuda.stream(st):  # the events of event_time_ms are recorded on st
+                for form, nb, d2h, h2d in (
+                        ("one_1GiB_copy", 1 << 30, lambda: probe_h.copy_(probe, non_blocking=True),
+                         lambda: probe.copy_(probe_h, non_blocking=True)),
+                        ("four_512MiB_copies", 1 << 31, lambda: chunked(probe_h, probe),
+                         lambda: chunked(probe, probe_h))):
+                    _, d2h_runs = event_time_ms(d2h, LINK_PROBES, 1)
+                    _, h2d_runs = event_time_ms(h2d, LINK_PROBES, 1)
+                    rates[f"{form}_{where}"] = {"d2h_gbps": round(nb / (min(d2h_runs) * 1e-3) / 1e9, 2),
+                                                "h2d_gbps": round(nb / (min(h2d_runs) * 1e-3) / 1e9, 2)}
+        return rates
+
+    probe_rates = {"before": probe_link()}
     host = stager.offload(ev_ids)  # allocates the pinned buffers
     host.event.synchronize()
     results = []
@@ -660,10 +681,15 @@ def run_offload(args, dev):
     b3.record(stager.stream)
     torch.cuda.synchronize()
     pre_ms = a3.elapsed_time(b3)
+    probe_rates["after"] = probe_link()
+    peak_d2h = max(r["d2h_gbps"] for when in probe_rates.values() for r in when.values())
+    peak_h2d = max(r["h2d_gbps"] for when in probe_rates.values() for r in when.values())
     ok = all(torch.equal(pool.k_cache[l, new_ids.to(dev).long()], pool.k_cache[l, ev_ids[l].to(dev).long()]) and
              torch.equal(pool.v_cache[l, new_ids.to(dev).long()], pool.v_cache[l, ev_ids[l].to(dev).long()])
              for l in range(L))
     rt = sorted(results)[len(results) // 2]
+    off_gbps = nbytes / (off_ms * 1e-3) / 1e9
+    pre_gbps = nbytes / (pre_ms * 1e-3) / 1e9
     return {
         "metric": "Config 5b offload+prefetch round trip GB/s (each direction)",
         "value": round(2 * nbytes / (rt * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
@@ -672,16 +698,24 @@ def run_offload(args, dev):
         "config": {"workload": "offload_config5b", "layers": L, "batch": B, "evicted_pages_per_layer": n,
                    "bytes_each_way": nbytes},
         "bit_exact": bool(ok),
-        "offload_gbps": round(nbytes / (off_ms * 1e-3) / 1e9, 2),
-        "prefetch_gbps": round(nbytes / (pre_ms * 1e-3) / 1e9, 2),
-        "roofline": {"bound": "host link", "achieved": round(nbytes / (off_ms * 1e-3) / 1e9, 2),
-                     "peak": round(peak_d2h, 2), "unit": "GB/s",
-                     "frac": round(nbytes / (off_ms * 1e-3) / 1e9 / peak_d2h, 4), "traffic": None,
-                     "peak_h2d": round(peak_h2d, 2), "frac_h2d": round(nbytes / (pre_ms * 1e-3) / 1e9 / peak_h2d, 4),
-                     "peak_source": (f"fastest of {LINK_PROBES} 1 GiB pinned hipMemcpyAsync copies per direction in "
-                                     f"the same process"),
-                     "pcie_gen5_x16_gbps": PCIE_GEN5_X16_GBPS,
-                     "frac_of_pcie_gen5_x16": round(nbytes / (off_ms * 1e-3) / 1e9 / PCIE_GEN5_X16_GBPS, 4)},
+        "offload_gbps": round(off_gbps, 2),
+        "prefetch_gbps": round(pre_gbps, 2),
+        # The host link's published peak is the roofline; the fastest plain pinned copy measured
+        # here is reported beside it. (Under rocprofv3 the plain D2H copies measured 54.7 GB/s
+        # against 57.0 without it, while the stager's D2H stayed at 55.8 GB/s, so the second
+        # fraction can read above 1 in a profiled run.)
+        "roofline": {"bound": "host link", "achieved": round(off_gbps, 2), "peak": PCIE_GEN5_X16_GBPS,
+                     "unit": "GB/s", "frac": round(off_gbps / PCIE_GEN5_X16_GBPS, 4), "traffic": None,
+                     "peak_source": "PCIe Gen5 x16, one direction: 32 GT/s x 16 lanes, 128b/130b encoding",
+                     "achieved_h2d": round(pre_gbps, 2), "frac_h2d": round(pre_gbps / PCIE_GEN5_X16_GBPS, 4),
+                     "measured_copy_peak": {
+                         "d2h_gbps": round(peak_d2h, 2), "h2d_gbps": round(peak_h2d, 2),
+                         "frac_d2h": round(off_gbps / peak_d2h, 4), "frac_h2d": round(pre_gbps / peak_h2d, 4),
+                         "source": (f"fastest of {LINK_PROBES} runs per direction of plain pinned hipMemcpyAsync "
+                                    f"copies in the same process, one 1 GiB copy or four 512 MiB copies back "
+                                    f"to back, on the default and on the stager's stream, before and after "
+                                    f"the stager's runs"),
+                         "probe_forms": probe_rates}},
         "cpu_baseline": None,
     }
 
@@ -777,9 +811,10 @@ def run_offload_seq(args, dev):
                                      "seconds": round(ref_s, 3),
                                      "sample": "48 blocks x 32 layers of one sequence, offload direction: a pinned "
                                                "allocation and a copy per K and per V block"},
-        "roofline": {"bound": "host link", "achieved": round(gbps_off, 2), "peak": None, "unit": "GB/s",
-                     "frac": None, "traffic": None,
-                     "note": "see the offload workload for the measured pinned-copy peak (57 GB/s)"},
+        "roofline": {"bound": "host link", "achieved": round(gbps_off, 2), "peak": PCIE_GEN5_X16_GBPS,
+                     "unit": "GB/s", "frac": round(gbps_off / PCIE_GEN5_X16_GBPS, 4), "traffic": None,
+                     "peak_source": "PCIe Gen5 x16, one direction: 32 GT/s x 16 lanes, 128b/130b encoding",
+                     "note": "the offload workload also measures the fastest plain pinned copy (57 GB/s)"},
         "cpu_baseline": None,
     }
 
