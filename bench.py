@@ -701,9 +701,9 @@ def run_offload(args, dev):
         "offload_gbps": round(off_gbps, 2),
         "prefetch_gbps": round(pre_gbps, 2),
         # The host link's published peak is the roofline; the fastest plain pinned copy measured
-        # here is reported beside it. (Under rocprofv3 the plain D2H copies measured 54.7 GB/s
-        # against 57.0 without it, while the stager's D2H stayed at 55.8 GB/s, so the second
-        # fraction can read above 1 in a profiled run.)
+        # here is reported beside it. (Under rocprofv3 the probe's copies run as blit kernels,
+        # __amd_rocclr_copyBuffer, at 54.6 GB/s against 57.0 without it, while the stager's copies
+        # stay on the DMA engines at 56.9 GB/s, so that second fraction reads ~1.02 in a profiled run.)
         "roofline": {"bound": "host link", "achieved": round(off_gbps, 2), "peak": PCIE_GEN5_X16_GBPS,
                      "unit": "GB/s", "frac": round(off_gbps / PCIE_GEN5_X16_GBPS, 4), "traffic": None,
                      "peak_source": "PCIe Gen5 x16, one direction: 32 GT/s x 16 lanes, 128b/130b encoding",
