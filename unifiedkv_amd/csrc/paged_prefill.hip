@@ -99,11 +99,10 @@ __device__ __forceinline__ int kv_len_of(const PrefillArgs& a, int b) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
-// Two bf16 values -> two fp16 values (RNE; exact when 2^-14 <= |x| < 65520),
-// folding the magnitude bits of both into amag (bf16 magnitudes above 0x477F,
-// i.e. |x| >= 65536, inf and NaN, do not fit fp16).
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, u16x2& amag) {
-  amag = __builtin_elementwise_max(amag, as_u16x2(w & 0x7fff7fffu));
+// Two bf16 values -> two fp16 values (RNE; exact when 2^-14 <= |x| < 65520). A bf16 value
+// that fp16 cannot hold (|x| >= 65536, the next bf16 above 65280; inf; NaN) becomes an fp16
+// inf or NaN.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   return pack_f16(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
 }
 
@@ -301,9 +300,11 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       gload16(rv[i], a.v + (uint64_t)pg * (uint32_t)a.v_sp + voff[i]);
     }
   };
-  // The largest bf16 V magnitude this thread stored (as 16-bit patterns), over every tile:
-  // checked once after the loop for values fp16 cannot hold.
-  u16x2 amag = {0, 0};
+  // The largest and the smallest fp16 V value this thread stored, over every tile (three-input
+  // packed maximum / minimum, which carry a NaN through): checked once after the loop for an
+  // inf or NaN, i.e. a bf16 value fp16 cannot hold.
+  typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
+  hv2 vmax = {0, 0}, vmin = {0, 0};
   auto store = [&](int u, int slot, int id0, int id1, u32x4 (&rk)[ITEMS], u32x4 (&rv)[ITEMS]) {
     const bool full = page_ok(id0) && page_ok(id1) && kTileKeys * (u + 1) <= Lk;
     // The other register set's 2 * ITEMS loads were issued after this set's.
@@ -311,15 +312,24 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
     for (int i = 0; i < ITEMS; ++i) vm_wait<2 * ITEMS>(rk[i], rv[i]);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      u32x4 v = rv[i];
+      // (converted before the junk rows are zeroed: the conversion writes new registers, which
+      // the zeroing then selects in place, with no copy of the loaded ones)
+      u32x4 v;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = kBf16 ? bf16x2_to_f16x2(rv[i][c]) : rv[i][c];
       if (!full) {  // (wave-uniform) rows past the sequence or on an invalid page hold junk
         const bool ok = page_ok(lds_row[i] < 16 ? id0 : id1) && kTileKeys * u + lds_row[i] < Lk;
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = ok ? v[c] : 0u;
       }
       if constexpr (kBf16) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = bf16x2_to_f16x2(v[c], amag);
+        const uint32_t w0 = v[0], w1 = v[1], w2 = v[2], w3 = v[3];
+        const hv2 c0 = __builtin_bit_cast(hv2, w0), c1 = __builtin_bit_cast(hv2, w1);
+        const hv2 c2 = __builtin_bit_cast(hv2, w2), c3 = __builtin_bit_cast(hv2, w3);
+        vmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(vmax, c0), c1);
+        vmax = __builtin_elementwise_maximum(__builtin_elementwise_maximum(vmax, c2), c3);
+        vmin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(vmin, c0), c1);
+        vmin = __builtin_elementwise_minimum(__builtin_elementwise_minimum(vmin, c2), c3);
       }
       *reinterpret_cast<u32x4*>(&k_s[slot][lds_row[i]][8 * lds_ch[i]]) = rk[i];
       *reinterpret_cast<u32x4*>(&v_s[slot][lds_row[i]][8 * lds_ch[i]]) = v;
@@ -575,7 +585,10 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
-  const bool wide_mine = kBf16 && __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(amag, u16x2{0x477F, 0x477F})) != 0u;
+  // (an fp16 magnitude pattern above 0x7BFF, the largest finite one, is an inf or a NaN)
+  const u16x2 mag = __builtin_elementwise_max(as_u16x2(__builtin_bit_cast(uint32_t, vmax) & 0x7fff7fffu),
+                                              as_u16x2(__builtin_bit_cast(uint32_t, vmin) & 0x7fff7fffu));
+  const bool wide_mine = kBf16 && __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(mag, u16x2{0x7BFF, 0x7BFF})) != 0u;
   if (kBf16 && __syncthreads_or(wide_mine)) {
     prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, max(q0, 0), min(C, q0 + qw), wv, WAVES, lane);
     return;
