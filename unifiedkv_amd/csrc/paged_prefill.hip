@@ -358,13 +358,16 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
+  // Tiles t < n_full end below the sequence end and below every column's diagonal (key
+  // 32t + 31 <= min(Lk - 1, wpos_min)).
+  const int n_full = max(0, min(Lk, wpos_min + 1)) / kTileKeys;
   const float sl2 = a.scale_log2;
   const uint32_t ones_f16 = 0x3C003C00u;
 
   auto compute = [&](int t, int slot) {
     const int key0 = t * kTileKeys;
     const bool pg0 = page_ok(t_id[0][0]), pg1 = page_ok(t_id[0][1]);
-    const bool full = pg0 && pg1 && key0 + kTileKeys <= Lk && key0 + kTileKeys - 1 <= wpos_min;
+    const bool full = pg0 && pg1 && t < n_full;
     // S^T[key][column] for the tile's two 16-key blocks and every column block, masked. (As one
     // inlined function the register allocator keeps the three-column loop within 256 VGPRs with
     // no scratch under the iterative-ILP schedule this file is built with; written out in line,
