@@ -330,8 +330,9 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  *       j in [sink_len, L - obs_len), and the zero rows padding them to a multiple of 16, of
  *       2^(q.k_j * softmax_scale * log2(e)) (a zero row scores 0);
  *   obs_stats[2 * (b * stats_seq_stride + h * obs_len + i) + 1] = 0, or 1 where that sum fell
- *       below 2^-100 of the query's largest weight (its low bits are lost; ukv_snapkv_scores_from_stats
- *       recomputes such items).
+ *       below 2^-100 of the query's largest weight, or where the sink and window keys hold half of
+ *       the query's weight or more (its low bits are lost; ukv_snapkv_scores_from_stats recomputes
+ *       such items).
  * stats_seq_stride counts (value, flag) pairs and is at least num_q_heads * obs_len; obs_stats is
  * 8-byte aligned. For the layout ukv_snapkv_scores_from_stats reads ([seqs][layers][num_q_heads]
  * [obs_len] pairs) pass obs_stats + 2 * layer * num_q_heads * obs_len and stats_seq_stride =
@@ -340,13 +341,12 @@ int ukv_paged_prefill(const void* q, const void* k_cache, const void* v_cache, c
  * scores recompute them. C_b >= obs_len for the rows to exist.
  * The reference captures the window's queries in its q_proj hook (core/scheduler.py:269-341)
  * and normalises their softmax over K_mid at selection time (core/scheduler.py:565-592,
- * core/compress.py:116-130); here that normaliser is taken while the prefill streams the keys.
- * The query blocks that hold the window run in a second kernel, beside the prefill kernel, on a
- * library-owned stream of the current device (default priority) that the call forks from the given
- * stream and joins back into it with events: work enqueued on the given stream after the call sees
- * every result, and a call captured into a HIP graph records both kernels. The device's first such
- * call creates that stream and its two events (held until the process ends); make it outside graph
- * capture. Calls from several host threads on one device are serialised around the fork and join.
+ * core/compress.py:116-130); here that normaliser comes from the prefill's own softmax
+ * denominators: the prefill kernel leaves each window row's running max and denominator (the sum
+ * of its fp16-rounded weights over every key it sees) in obs_stats, and a second kernel on the
+ * same stream sums the sink and window keys' weights again (fp32, from the same scores) and takes
+ * them off. Relative error of the sum: that of fp16-rounded weights (2^-11 each, random sign), at
+ * most doubled by the difference before the row is flagged.
  */
 int ukv_paged_prefill_obs_stats(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                                 const int32_t* cu_seqlens_q, const int32_t* kv_lens, void* out, int batch,

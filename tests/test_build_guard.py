@@ -42,7 +42,8 @@ def test_parse_and_verdicts_on_fixed_remarks():
     assert bad[0].startswith("_ZN3ukv20paged_prefill_kernel") and "ScratchSize 20" in bad[0]
     assert bad[1].startswith("_ZN3ukv16snap_tile_kernel") and "VGPRs spilled 3" in bad[1]
     assert not _build.guarded("_ZN3ukv27paged_prefill_scalar_kernelILi1EEEvNS_11PrefillArgsE")
-    assert _build.guarded("_ZN3ukv26paged_prefill_stats_kernelILi0ELi8EEEvNS_11PrefillArgsE")
+    assert _build.guarded("_ZN3ukv20paged_prefill_kernelILi0ELi8ELb0EEEvNS_11PrefillArgsE")
+    assert not _build.guarded("_ZN3ukv22obs_rows_finish_kernelILi1EEEvNS_11PrefillArgsE")
 
 
 def test_incomplete_remarks_are_refused():

@@ -61,7 +61,7 @@ SOURCE_FLAGS: Dict[str, List[str]] = {
 # lanes of a VGPR the compiler reserves for that purpose touch no load destination and no
 # memory; once no such lane is left they go through scratch, which ScratchSize reports.)
 GUARDED_SOURCES = ("page16_decode.hip", "paged_prefill.hip", "snapkv_score.hip")
-GUARDED_KERNELS = ("page16_split_kernel", "paged_prefill_kernel", "paged_prefill_stats_kernel", "snap_tile_kernel")
+GUARDED_KERNELS = ("page16_split_kernel", "paged_prefill_kernel", "snap_tile_kernel")
 REMARK_FLAG = "-Rpass-analysis=kernel-resource-usage"
 
 _FN_RE = re.compile(r"remark: Function Name: (\S+)")

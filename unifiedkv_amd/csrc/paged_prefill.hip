@@ -41,10 +41,10 @@
 //     operands come from ds_read_b64_tr_b16 transpose reads; the softmax
 //     denominators come from one more MFMA against a ones operand, so they sum
 //     exactly the rounded P;
-//   * SnapKV row statistics: the two-column blocks holding each sequence's
-//     last obs queries run in a kernel of their own (paged_prefill_stats_kernel),
-//     which also sums the middle keys' fp32 weights; it runs beside the prefill
-//     kernel on a side stream forked from and joined back into the caller's.
+//   * SnapKV row statistics: the blocks holding each sequence's last obs queries
+//     also write those rows' running max and denominator; obs_rows_finish_kernel
+//     then sums the sink and window keys' weights again from the same scores and
+//     takes them off, leaving the middle keys' sum.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -72,22 +72,21 @@ struct PrefillArgs {
   const int32_t* cu_q;     // [B+1]
   const int32_t* kv_lens;  // [B] keys per sequence, the chunk included
   int B, Hq, n_rep, n_groups, D, max_blocks, num_pages;
-  // Query blocks of every (sequence, KV group), from q_skip queries below the end of its chunk
-  // down: n3 blocks of three column blocks per wave, then n2 of two. Blocks that reach below the
-  // chunk's first query are partial or empty (chunks shorter than the longest). The three-column
-  // blocks of every pair are dispatched in a first pass, the two-column ones in a second. With
-  // statistics (obs > 0), the last q_skip = n_s * (two-column block) queries of each chunk are the
-  // n_s blocks of the statistics kernel, launched beside it.
-  int n3, n2, q_skip, n_s;
+  // Query blocks of every (sequence, KV group), from the end of its chunk down: n3 blocks of three
+  // column blocks per wave, then n2 of two. Blocks that reach below the chunk's first query are
+  // partial or empty (chunks shorter than the longest). The three-column blocks of every pair are
+  // dispatched in a first pass, the two-column ones in a second.
+  int n3, n2;
   // The longest chunk the caller declared: the block plan covers that many queries. A chunk
   // longer than it gets NaN in every row of its output (its K/V were not all written either).
   int max_chunk;
   float scale, scale_log2;
-  // SnapKV observation statistics (obs > 0): the query blocks that hold a sequence's last obs
-  // queries run in the statistics kernel, which also writes, for each of those queries and q head
+  // SnapKV observation statistics (obs > 0): for each of a sequence's last obs queries and q head
   // h, the log2-sum-exp2 of its scaled scores over the middle keys [sink, L - obs) and the zero
   // rows that pad them to a multiple of 16 keys: obs_stats[b * stats_seq_stride + h * obs + i].x
   // (.y = 0, or 1 where the sum lost precision), the row statistics the SnapKV scoring pass takes.
+  // The prefill kernel leaves each row's (max, denominator) there and obs_rows_finish_kernel
+  // takes the sink and window keys' share off.
   float2* obs_stats;
   int64_t stats_seq_stride;
   int sink, obs;
@@ -186,6 +185,19 @@ __device__ void prefill_pairs_fp32(const PrefillArgs& a, int b, int g, int q_beg
   }
 }
 
+// Flags (y = 1) the observation rows among queries lo .. hi - 1 of sequence b's chunk (C
+// queries), q heads of KV group g, for the scoring pass to recompute from the keys.
+template <int WAVES>
+__device__ void flag_obs_rows(const PrefillArgs& a, int b, int g, int C, int lo, int hi) {
+  lo = max(lo, C - a.obs);
+  const int n = max(0, min(hi, C) - lo) * a.n_rep;
+  for (int t = threadIdx.x; t < n; t += 64 * WAVES) {
+    const int qi = lo + t / a.n_rep, h = g * a.n_rep + t % a.n_rep;
+    if (qi >= 0 && h < a.Hq)
+      a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)h * a.obs + (qi - (C - a.obs))] = make_float2(NAN, 1.f);
+  }
+}
+
 // LDS of one workgroup: kStages ring slots of K and V (fp16) tiles.
 struct PrefillLds {
   __attribute__((aligned(16))) uint16_t k_s[kStages][kTileKeys][kRowPad];
@@ -193,18 +205,18 @@ struct PrefillLds {
 };
 
 // The query block q0 .. q0 + QW - 1 (QW = WAVES * CB * 16 / n_rep; q0 may be negative) of
-// sequence b, KV group g, with CB 16-column blocks per wave. STATS: a block holding some of the
-// sequence's last obs queries (two column blocks per wave), which also produces those queries'
-// SnapKV row statistics.
-template <int DT, int WAVES, bool STATS, int CB>
+// sequence b, KV group g, with CB 16-column blocks per wave. ROWS: also write, for each of the
+// sequence's last obs queries in the block and each q head h, the pair (m, l) of the column's
+// running max m (log2 units) and its softmax denominator l (the sum of the fp16 weights
+// 2^(s * scale * log2e - m) over every key the query sees) into
+// obs_stats[b * stats_seq_stride + h * obs + i], for obs_rows_finish_kernel.
+template <int DT, int WAVES, bool ROWS, int CB>
 __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, const int g, const int q0,
                                              PrefillLds& lds) {
   constexpr int D = 128;
   constexpr int STEPS = D / 32;
   constexpr int NT = 64 * WAVES;
   constexpr int ITEMS = kTileKeys * 16 / NT;  // 16-byte chunks per thread per tensor per tile
-  // The STATS instance holds two column blocks, which leaves registers for its sums.
-  static_assert(!STATS || CB == 2, "statistics blocks hold two column blocks per wave");
   constexpr float kTau = 8.f;
   constexpr bool kBf16 = DT == UKV_DTYPE_BF16;
   static_assert(ITEMS * NT == kTileKeys * 16, "loader mapping");
@@ -249,13 +261,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
   float m_ref[CB];  // running max of the column (log2 units)
   f32x4 o[CB][8];
   f32x4 lacc[CB];  // softmax denominators of columns 4*kg + r
-  // STATS: this lane's fp32 sum of 2^(s - m_ref) over its middle keys of column i16, and the
-  // current tile's share (added once the tile's max has settled).
-  float lmid[STATS ? CB : 1], tsum[STATS ? CB : 1];
-  const int mid_end = STATS ? Lk - a.obs : 0;
-  if constexpr (STATS)
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) lmid[cb] = 0.f;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     m_ref[cb] = kNegFltMax;
@@ -407,9 +412,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
     // like their values, and inf and NaN lie above), and a column block whose
     // max moved is rescaled and its P recomputed.
     u32x4 pa[CB];
-    // STATS: is the tile's key kb*16 + 4kg + r one of the middle keys [sink, L - obs)?
-    const bool mid_all = STATS && key0 >= a.sink && key0 + kTileKeys <= mid_end;
-    const bool mid_none = !STATS || key0 + kTileKeys <= a.sink || key0 >= mid_end;
     auto exp_pack = [&](int cb) {
       float p[2][4];
 #pragma unroll
@@ -418,26 +420,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
         for (int r = 0; r < 4; ++r) p[kb][r] = fast_exp2(__builtin_fmaf(sacc[kb][cb][r], sl2, -m_ref[cb]));
       pa[cb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                      pack_f16(p[1][2], p[1][3])};
-      if constexpr (STATS) {
-        // (mid_all and mid_none are wave-uniform: only the tiles straddling a boundary mask)
-        float ts = 0.f;
-        if (mid_all) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ts += p[kb][r];
-        } else if (!mid_none) {
-          const int lo = a.sink - key0 - 4 * kg, hi = mid_end - key0 - 4 * kg;  // this lane's middle offsets
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int d = kb * 16 + r;
-              ts += ((d >= lo) & (d < hi)) ? p[kb][r] : 0.f;
-            }
-        }
-        tsum[cb] = ts;
-      }
     };
     // Moves column block cb's max to the tile's where that lies more than kTau above it,
     // rescaling what was summed under the old one; returns whether it moved.
@@ -460,7 +442,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[cb][e][r] *= ar;
       }
-      if constexpr (STATS) lmid[cb] *= alpha;  // lane-local: column i16, like m_ref
       return true;
     };
     // The weights and the vote run at raised wave priority: when the SIMD's other wave is
@@ -492,9 +473,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
           if (settle(cb)) exp_pack(cb);
       }
     }
-    if constexpr (STATS)
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) lmid[cb] += tsum[cb];
     __builtin_amdgcn_s_setprio(0);
     // P.V: the B operand of output tile e (dims 16e .. 16e + 15) holds, in lane
     // (i16, kg), dim 16e + i16 of keys 4kg..4kg+3 and 16+4kg..16+4kg+3 (the
@@ -560,32 +538,6 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
     vm_wait<0>(rk1[i], rv1[i]);
   }
 
-  if constexpr (STATS) {
-    // Row statistics of the observation queries: log2 of the sum over the middle keys and the
-    // n_pad zero rows (score 0) that pad them to whole 16-key blocks, in the units of
-    // s * scale * log2(e). Column i16 of each column block; the 4 lane groups hold its keys.
-    const int L_mid = Lk - a.sink - a.obs;
-    const int n_pad = ((L_mid + 15) & ~15) - L_mid;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      float l = lmid[cb] + __shfl_xor(lmid[cb], 16);
-      l += __shfl_xor(l, 32);
-      const int qi = wq0 + cb * qpb + i16 / a.n_rep;
-      const int hh = g * a.n_rep + i16 % a.n_rep;
-      if (wave_live && kg == 0 && qi >= C - a.obs && qi >= 0 && qi < C && hh < a.Hq) {
-        const float m = m_ref[cb];
-        const float top = n_pad > 0 ? fmaxf(m, 0.f) : m;
-        const float lse = top + __log2f(l * exp2f(m - top) + (float)n_pad * exp2f(-top));
-        // m is the max over every key the query sees, the sink and window included: middle
-        // weights below 2^-126 of it lose bits, so a sum under 2^-100 marks the row (y = 1)
-        // for the scoring pass to recompute from the keys.
-        const bool exact = l >= 0x1p-100f && __builtin_isfinite(lse);
-        a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)hh * a.obs + (qi - (C - a.obs))] =
-            make_float2(lse, exact ? 0.f : 1.f);
-      }
-    }
-  }
-
   // A bf16 V value that fp16 cannot hold anywhere in this workgroup's keys:
   // recompute its columns on the fp32 fallback.
   // (an fp16 magnitude pattern above 0x7BFF, the largest finite one, is an inf or a NaN)
@@ -593,12 +545,13 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
                                               as_u16x2(__builtin_bit_cast(uint32_t, vmin) & 0x7fff7fffu));
   const bool wide_mine = kBf16 && __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(mag, u16x2{0x7BFF, 0x7BFF})) != 0u;
   if (kBf16 && __syncthreads_or(wide_mine)) {
+    if constexpr (ROWS) flag_obs_rows<WAVES>(a, b, g, C, max(q0, 0), min(C, q0 + qw));
     prefill_pairs_fp32<DT>(a, b, g, q_begin, C, P0, Lk, max(q0, 0), min(C, q0 + qw), wv, WAVES, lane);
     return;
   }
 
   // out[column] = o / l: lane (i16, kg) holds dims 16e + i16 of columns 4*kg + r,
-// and lacc[cb][r] is the denominator of column 4*kg + r.
+  // and lacc[cb][r] is the denominator of column 4*kg + r (the same in its 16 lanes).
   if (!wave_live) return;
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -607,11 +560,17 @@ __device__ __forceinline__ void prefill_tile(const PrefillArgs& a, const int b, 
       const int col = 4 * kg + r;
       const int qi = wq0 + cb * qpb + col / a.n_rep;
       const int hh = g * a.n_rep + col % a.n_rep;
+      // ROWS: the column's running max, held by lane col (column i16 = col)
+      const float m_col = ROWS ? __shfl(m_ref[cb], col) : 0.f;
       if (qi >= 0 && qi < C && hh < a.Hq) {
         const float inv = 1.f / lacc[cb][r];
         uint16_t* orow = a.out + ((int64_t)(q_begin + qi) * a.Hq + hh) * D + i16;
 #pragma unroll
         for (int e = 0; e < 8; ++e) orow[16 * e] = Elem<DT>::from_float(o[cb][e][r] * inv);
+        if constexpr (ROWS)
+          if (i16 == 0 && qi >= C - a.obs)
+            a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)hh * a.obs + (qi - (C - a.obs))] =
+                make_float2(m_col, lacc[cb][r]);
       }
     }
   }
@@ -678,10 +637,9 @@ __device__ __forceinline__ void xcd_range(int total, int xcd, int& start, int& e
 // after pair. Each XCD takes a contiguous range of these numbers, so that the blocks of one pair
 // share that XCD's L2 while they stream its pages, and dispatches the three-column blocks of its
 // pairs before their two-column blocks: the cheaper blocks then fill the last round of the launch.
-// SKIP: the blocks end q_skip queries below each chunk's end, where the statistics kernel's blocks
-// take over. (Launches without statistics take the instance without it, whose two-column loop the
-// compiler schedules better: the unknown q_skip cost those blocks ~4 %.)
-template <int DT, int WAVES, bool SKIP>
+// ROWS: the blocks also write the (m, l) pairs of the chunk's last obs queries (prefill_tile),
+// which obs_rows_finish_kernel turns into SnapKV row statistics.
+template <int DT, int WAVES, bool ROWS>
 __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
 paged_prefill_kernel(const PrefillArgs a) {
   __shared__ PrefillLds lds;
@@ -691,51 +649,115 @@ paged_prefill_kernel(const PrefillArgs a) {
   if (!locate_item(start, end, n_items, a.n3, blockIdx.x >> 3, pair, j)) return;  // (never: the grid holds total)
   const int g = pair % a.n_groups, b = pair / a.n_groups;
   const int C = a.cu_q[b + 1] - a.cu_q[b];
-  const int top = C - (SKIP ? a.q_skip : 0);  // the blocks end here
   const int qpb = 16 / a.n_rep;
   const int qw2 = WAVES * 2 * qpb, qw3 = WAVES * 3 * qpb;
   if (C > a.max_chunk) {
-    const int q0 = j < a.n3 ? top - qw3 * (j + 1) : top - qw3 * a.n3 - qw2 * (j - a.n3 + 1);
+    const int q0 = j < a.n3 ? C - qw3 * (j + 1) : C - qw3 * a.n3 - qw2 * (j - a.n3 + 1);
     const int q1 = min(C, j < a.n3 ? q0 + qw3 : q0 + qw2);
-    prefill_nan_rows<WAVES>(a, b, g, j == n_items - 1 ? 0 : max(0, q0), q1);
+    const int lo = j == n_items - 1 ? 0 : max(0, q0);
+    prefill_nan_rows<WAVES>(a, b, g, lo, q1);
+    if constexpr (ROWS) flag_obs_rows<WAVES>(a, b, g, C, lo, q1);
     return;
   }
   if (j < a.n3)
-    prefill_tile<DT, WAVES, false, 3>(a, b, g, top - qw3 * (j + 1), lds);
+    prefill_tile<DT, WAVES, ROWS, 3>(a, b, g, C - qw3 * (j + 1), lds);
   else
-    prefill_tile<DT, WAVES, false, 2>(a, b, g, top - qw3 * a.n3 - qw2 * (j - a.n3 + 1), lds);
+    prefill_tile<DT, WAVES, ROWS, 2>(a, b, g, C - qw3 * a.n3 - qw2 * (j - a.n3 + 1), lds);
 }
 
-// The statistics blocks: the n_s two-column blocks at the end of each pair's chunk, which hold
-// its last obs queries. A kernel of their own, launched beside paged_prefill_kernel: built into
-// one kernel, the statistics code changed the compiler's register allocation and schedule of the
-// three-column blocks' loop, which then ran ~10 % slower. Each XCD runs the statistics blocks of
-// the pairs whose other blocks it runs in paged_prefill_kernel (for the same number of pairs), so
-// both read a pair's pages through one L2.
-template <int DT, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
-paged_prefill_stats_kernel(const PrefillArgs a) {
-  __shared__ PrefillLds lds;
-  int start, end;
-  xcd_range(a.n_s * a.n_groups * a.B, blockIdx.x & 7, start, end);
-  const int item = start + (blockIdx.x >> 3);
-  if (item >= end) return;  // (never: the grid holds total)
-  const int pair = item / a.n_s, js = item % a.n_s;
-  const int g = pair % a.n_groups, b = pair / a.n_groups;
-  const int C = a.cu_q[b + 1] - a.cu_q[b];
-  const int qw2 = WAVES * 2 * (16 / a.n_rep);
-  const int q0 = C - qw2 * (js + 1);
-  if (C > a.max_chunk) {  // (see prefill_nan_rows); the rows' statistics are flagged for the scorer
-    const bool lowest = js == a.n_s - 1 && a.n3 + a.n2 == 0;
-    prefill_nan_rows<WAVES>(a, b, g, lowest ? 0 : max(0, q0), min(C, q0 + qw2));
-    for (int i = threadIdx.x; i < a.n_rep * qw2; i += 64 * WAVES) {
-      const int qi = q0 + i / a.n_rep, h = g * a.n_rep + i % a.n_rep;
-      if (qi >= max(0, C - a.obs) && qi < C && h < a.Hq)
-        a.obs_stats[(int64_t)b * a.stats_seq_stride + (int64_t)h * a.obs + (qi - (C - a.obs))] = make_float2(NAN, 1.f);
+// SnapKV row statistics from the (m, l) pairs paged_prefill_kernel<..., true> left in obs_stats.
+// l sums the weights 2^(s * scale * log2e - m) of every key the query sees, each rounded to fp16;
+// the sink keys [0, sink) and the window keys [max(L - obs, sink), the query's own position] are
+// summed again here from the same scores (v_mfma_f32_16x16x32 on the same operands, in the same
+// order), exp2 and fp16 rounding, and taken off, which leaves the middle keys [sink, L - obs).
+// Where the prefill computed those weights against the final m (m moves only when a weight would
+// reach 2^8), they cancel exactly and the sum carries only the middle weights' own fp16 rounding;
+// weights taken before a later move of m were rescaled in fp32 and leave a residue of at most
+// 2^-11 of their share. The row becomes (log2 of that sum and of
+// the zero rows padding the middle keys to a multiple of 16, 0) in the units of s * scale * log2e;
+// it is flagged (y = 1) for the scoring pass to recompute from the keys where the prefill flagged
+// it, where the sink and window hold half of its weight or more (the difference would lose bits),
+// or where the middle sum falls below 2^-100 of its max (m is the max over every key the query
+// sees: middle weights below 2^-126 of it lose bits). One wave per 16 columns (observation query,
+// q head of the group) of a (sequence, KV group); lane (i16, kg) holds column i16 and keys
+// 4kg .. 4kg + 3 of each 16-key page. (The (m, l) pairs exist only where the tiled kernel ran.)
+template <int DT>
+__global__ void __launch_bounds__(256) obs_rows_finish_kernel(const PrefillArgs a) {
+  const int lane = threadIdx.x & 63, i16 = lane & 15, kg = lane >> 4;
+  const int cols = a.obs * a.n_rep;
+  const int nblk = (cols + 15) >> 4;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)a.B * a.n_groups * nblk) return;  // (wave-uniform)
+  const int blk = (int)(w % nblk);
+  const int64_t pair = w / nblk;
+  const int g = (int)(pair % a.n_groups), b = (int)(pair / a.n_groups);
+  const int q_begin = a.cu_q[b], C = a.cu_q[b + 1] - q_begin;
+  const int L = kv_len_of(a, b);
+  const int col = blk * 16 + i16;
+  const int i = col / a.n_rep, h = g * a.n_rep + col % a.n_rep;
+  const int qi = C - a.obs + i;
+  const bool live = col < cols && h < a.Hq && qi >= 0 && C <= a.max_chunk;
+  float2* slot = a.obs_stats + (int64_t)b * a.stats_seq_stride + (int64_t)h * a.obs + i;
+  const float2 ml = live ? *slot : make_float2(0.f, 0.f);
+  const bool ok = live && __builtin_isfinite(ml.x) && ml.y > 0.f && __builtin_isfinite(ml.y);
+  const float m = ok ? ml.x : 0.f;
+  // B operand: dims 32s + 8kg .. 32s + 8kg + 7 of column i16's query row
+  const uint16_t* qp =
+      a.q + (int64_t)(q_begin + (live ? qi : 0)) * a.q_st + (int64_t)(live ? h : 0) * a.q_sh + 8 * kg;
+  u32x4 qv[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qv[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+  const int pos = L - C + qi;  // the query's position: it sees keys 0 .. pos
+  const float sl2 = a.scale_log2;
+  const int32_t* btrow = a.bt + (int64_t)b * a.max_blocks;
+  float part = 0.f;
+  // Keys [lo, hi) of pages p0 .. p1 - 1 (page pg holds keys 16 pg .. 16 pg + 15), four pages at a
+  // time with their loads issued together. A operand: dims 32s + 8kg .. of key 16 pg + i16.
+  auto pages = [&](int p0, int p1, int lo, int hi) {
+    for (int pg = p0; pg < p1; pg += 4) {
+      u32x4 ka[4][4];
+      bool pok[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int id = pg + u < p1 ? btrow[pg + u] : -1;
+        pok[u] = (unsigned)id < (unsigned)a.num_pages;
+        const uint16_t* kp =
+            a.k + (int64_t)(pok[u] ? id : 0) * a.k_sp + (int64_t)i16 * a.k_st + (int64_t)g * a.k_sh + 8 * kg;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ka[u][s] = pok[u] ? ld16(kp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma16x16x32<DT>(ka[u][s], qv[s], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * (pg + u) + 4 * kg + r;
+          // the weight rounded to fp16 as the prefill kernel summed it (see above)
+          const float p = (float)(_Float16)fast_exp2(__builtin_fmaf(acc[r], sl2, -m));
+          part += (pok[u] && key >= lo && key < hi && key <= pos) ? p : 0.f;
+        }
+      }
     }
-    return;
+  };
+  const int s_end = min(a.sink, L), w_beg = max(L - a.obs, a.sink);
+  pages(0, (s_end + 15) >> 4, 0, s_end);
+  pages(w_beg >> 4, (L + 15) >> 4, w_beg, L);
+  part += __shfl_xor(part, 16);
+  part += __shfl_xor(part, 32);
+  if (kg == 0 && live) {
+    float2 res = make_float2(0.f, 1.f);
+    if (ok) {
+      const float l = ml.y - part;
+      const int L_mid = L - a.sink - a.obs;
+      const int n_pad = ((L_mid + 15) & ~15) - L_mid;
+      const float top = n_pad > 0 ? fmaxf(m, 0.f) : m;
+      const float lse = top + __log2f(l * exp2f(m - top) + (float)n_pad * exp2f(-top));
+      if (l >= 0.5f * ml.y && l >= 0x1p-100f && __builtin_isfinite(lse)) res = make_float2(lse, 0.f);
+    }
+    *slot = res;
   }
-  prefill_tile<DT, WAVES, true, 2>(a, b, g, q0, lds);
 }
 
 // Marks every observation row of the call as recomputed-by-the-scorer: (0, 1) at row
@@ -966,27 +988,25 @@ extern "C" int ukv_kv_write_varlen(void* k_pool_layer, void* v_pool_layer, const
 namespace {
 
 // Block plan of the tiled prefill: the numbers n3 and n2 of three- and two-column query blocks
-// per (sequence, KV group) that cover its chunk's max_chunk queries (those below the statistics
-// blocks). A launch runs in rounds of one block per CU; the plan with the shortest predicted
-// launch is taken, modelling every block as streaming equally many keys (a long prefix) at its
+// per (sequence, KV group) that cover its chunk's max_chunk queries. A launch runs in rounds of
+// one block per CU; the plan with the shortest predicted launch is taken, modelling every block as streaming equally many keys (a long prefix) at its
 // measured cost relative to a three-column block (two columns 0.79: single blocks timed over the
-// same 32768 keys; statistics blocks 0.84: launches with forced plans), and each XCD's CUs as
-// taking the XCD's blocks in the kernel's order, each CU the next block once free, after the n_s
-// statistics blocks per pair that the statistics kernel (launched first, beside it) puts there.
+// same 32768 keys), and each XCD's CUs as taking the XCD's blocks in the kernel's order, each CU
+// the next block once free.
 struct BlockPlan {
   int n3, n2;
 };
 
-double plan_makespan(int64_t pairs, int n3, int n2, int n_s, int cus_per_xcd) {
+double plan_makespan(int64_t pairs, int n3, int n2, int cus_per_xcd) {
   const int n_items = n3 + n2;
-  const int64_t total = pairs * n_items, total_s = pairs * n_s;
+  const int64_t total = pairs * n_items;
   const int64_t per = total / 8, rem = total % 8;
   double worst = 0.0;
   std::vector<double> order;
   for (int x = 0; x < 8; ++x) {
     const int64_t start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
     const int64_t end = start + per + (x < rem ? 1 : 0);
-    order.assign(total_s / 8 + (x < total_s % 8 ? 1 : 0), 0.84);
+    order.clear();
     if (end > start)
       for (int pass = 0; pass < 2; ++pass)
         for (int64_t p = start / n_items; p <= (end - 1) / n_items; ++p) {
@@ -1008,23 +1028,23 @@ double plan_makespan(int64_t pairs, int n3, int n2, int n_s, int cus_per_xcd) {
   return worst;
 }
 
-BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int n_s, int cus_per_xcd) {
+BlockPlan choose_plan(int max_chunk, int64_t pairs, int qw2, int qw3, int cus_per_xcd) {
   const int n3_max = (std::max(0, max_chunk) + qw3 - 1) / qw3;
   BlockPlan best{n3_max, 0};
   // Large launches run many rounds, where the last one matters little: keep three-column blocks.
-  if (pairs * (n3_max + n_s) > (1 << 16) || cus_per_xcd <= 0 || n3_max == 0) return best;
+  if (pairs * n3_max > (1 << 16) || cus_per_xcd <= 0 || n3_max == 0) return best;
   static std::mutex mu;
-  static std::map<std::tuple<int, int64_t, int, int, int>, BlockPlan> cache;
-  const auto key = std::make_tuple(max_chunk, pairs, qw2, n_s, cus_per_xcd);
+  static std::map<std::tuple<int, int64_t, int, int>, BlockPlan> cache;
+  const auto key = std::make_tuple(max_chunk, pairs, qw2, cus_per_xcd);
   std::lock_guard<std::mutex> lock(mu);
   const auto hit = cache.find(key);
   if (hit != cache.end()) return hit->second;
-  double best_t = plan_makespan(pairs, n3_max, 0, n_s, cus_per_xcd);
+  double best_t = plan_makespan(pairs, n3_max, 0, cus_per_xcd);
   // Each three-column block traded for two-column ones adds work (0.79 x 1.5 > 1): a dozen
   // trades fill any last round.
   for (int n3 = n3_max - 1; n3 >= std::max(0, n3_max - 12); --n3) {
     const int n2 = (max_chunk - n3 * qw3 + qw2 - 1) / qw2;
-    const double t = plan_makespan(pairs, n3, n2, n_s, cus_per_xcd);
+    const double t = plan_makespan(pairs, n3, n2, cus_per_xcd);
     if (t < best_t - 1e-9) {
       best_t = t;
       best = BlockPlan{n3, n2};
@@ -1048,41 +1068,6 @@ int cus_per_xcd() {
     cached[dev].store(per, std::memory_order_relaxed);
   }
   return per;
-}
-
-// A stream per device for the statistics kernel, which runs beside the prefill kernel: forked
-// from the caller's stream and joined back into it with two events, under one lock per device so
-// that calls from several host threads do not interleave their fork and join. Created at the
-// device's first call with statistics (a call that is not being captured into a graph), held until
-// the process ends, at the default priority.
-struct SideStream {
-  std::mutex mu;
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-
-SideStream* side_stream() {
-  static SideStream side[64];
-  static std::mutex init_mu;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(init_mu);
-  SideStream& ss = side[dev];
-  if (!ss.stream) {
-    hipStream_t st = nullptr;
-    hipEvent_t f = nullptr, j = nullptr;
-    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-      if (f) (void)hipEventDestroy(f);
-      (void)hipStreamDestroy(st);
-      return nullptr;
-    }
-    ss.fork = f;
-    ss.join = j;
-    ss.stream = st;
-  }
-  return &ss;
 }
 
 struct ObsStats {
@@ -1156,46 +1141,30 @@ int prefill_impl(const void* q, const void* k_cache, const void* v_cache, const 
     constexpr int W = UKV_PREFILL_WAVES;
     const int qw2 = W * 2 * (16 / n_rep), qw3 = W * 3 * (16 / n_rep);
     const int64_t pairs = (int64_t)n_groups * batch;
-    // the statistics blocks cover the last obs queries; the prefill kernel's blocks the rest
-    a.n_s = obs ? (a.obs + qw2 - 1) / qw2 : 0;
-    a.q_skip = a.n_s * qw2;
-    const BlockPlan plan = choose_plan(max_chunk - a.q_skip, pairs, qw2, qw3, a.n_s, cus_per_xcd());
+    const BlockPlan plan = choose_plan(max_chunk, pairs, qw2, qw3, cus_per_xcd());
     a.n3 = plan.n3;
     a.n2 = plan.n2;
-    const int64_t wgs = (int64_t)(a.n3 + a.n2) * pairs, wgs_s = (int64_t)a.n_s * pairs;
-    if (wgs > INT32_MAX || wgs_s > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
-    auto launch_main = [&](hipStream_t st) {
-      if (dtype == UKV_DTYPE_BF16 && wgs_s)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
+    const int64_t wgs = (int64_t)(a.n3 + a.n2) * pairs;
+    const int64_t finish_waves = obs ? (int64_t)batch * n_groups * ((a.obs * n_rep + 15) / 16) : 0;
+    if (wgs > INT32_MAX || (finish_waves + 3) / 4 > INT32_MAX) return UKV_ERR_INVALID_ARGUMENT;
+    if (wgs > 0) {
+      // With statistics, the prefill kernel writes the observation rows' (m, l) pairs and
+      // obs_rows_finish_kernel, next on the same stream, turns them into the rows.
+      if (dtype == UKV_DTYPE_BF16 && obs)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
       else if (dtype == UKV_DTYPE_BF16)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
-      else if (wgs_s)
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_BF16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+      else if (obs)
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, true>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
       else
-        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, st, a);
-    };
-    auto launch_stats = [&](hipStream_t st) {
+        hipLaunchKernelGGL((paged_prefill_kernel<UKV_DTYPE_F16, W, false>), dim3((unsigned)wgs), dim3(64 * W), 0, stream, a);
+    }
+    if (finish_waves > 0) {
+      const dim3 fgrid((unsigned)((finish_waves + 3) / 4));
       if (dtype == UKV_DTYPE_BF16)
-        hipLaunchKernelGGL((paged_prefill_stats_kernel<UKV_DTYPE_BF16, W>), dim3((unsigned)wgs_s), dim3(64 * W), 0, st,
-                           a);
+        hipLaunchKernelGGL(obs_rows_finish_kernel<UKV_DTYPE_BF16>, fgrid, dim3(256), 0, stream, a);
       else
-        hipLaunchKernelGGL((paged_prefill_stats_kernel<UKV_DTYPE_F16, W>), dim3((unsigned)wgs_s), dim3(64 * W), 0, st,
-                           a);
-    };
-    if (wgs_s == 0) {
-      if (wgs > 0) launch_main(stream);
-    } else if (wgs == 0) {
-      launch_stats(stream);
-    } else {
-      SideStream* ss = side_stream();
-      if (!ss) return UKV_ERR_LAUNCH;
-      std::lock_guard<std::mutex> lock(ss->mu);
-      if (hipEventRecord(ss->fork, stream) != hipSuccess || hipStreamWaitEvent(ss->stream, ss->fork, 0) != hipSuccess)
-        return UKV_ERR_LAUNCH;
-      launch_stats(ss->stream);
-      if (hipEventRecord(ss->join, ss->stream) != hipSuccess) return UKV_ERR_LAUNCH;
-      launch_main(stream);
-      if (hipStreamWaitEvent(stream, ss->join, 0) != hipSuccess) return UKV_ERR_LAUNCH;
+        hipLaunchKernelGGL(obs_rows_finish_kernel<UKV_DTYPE_F16>, fgrid, dim3(256), 0, stream, a);
     }
   } else {
     const dim3 grid(total_q, num_q_heads);
