@@ -350,6 +350,39 @@ def test_understated_max_chunk_on_device_lengths_gives_nan_rows(cuda, path):
 
 
 @pytest.mark.gpu
+def test_statistics_rows_of_chunks_shorter_than_the_window_are_left_alone(cuda):
+    """Through the C entry point (the Python wrapper refuses such chunks): a sequence whose chunk
+    holds fewer than obs_len queries has window rows only for the queries it holds (none for an
+    empty chunk); the other slots keep what they held. A sequence whose keys all lie in the sink
+    has an empty middle: its rows are flagged. The attention output is the plain prefill's."""
+    import torch
+
+    from unifiedkv_amd import _ext, prefill, snapkv
+
+    case = make_case(62, [300, 40, 10], [150, 0, 5], Hq=8, Hkv=2, D=128)
+    t = to_dev(case, cuda)
+    prefill.write_chunk_kv(t["k_cache"], t["v_cache"], t["k_new"], t["v_new"], t["block_table"], t["cu"], t["kv_lens"],
+                           max(case["chunk"]))
+    st = snapkv.ObsStats(3, 1, 8, sink_len=16, obs_len=16, softmax_scale=case["scale"], device=cuda)
+    st.data.fill_(-7.0)
+    out = torch.empty_like(t["q"])
+    code = _ext.load().ukv_paged_prefill_obs_stats(
+        t["q"].data_ptr(), t["k_cache"].data_ptr(), t["v_cache"].data_ptr(), t["block_table"].data_ptr(),
+        t["cu"].data_ptr(), t["kv_lens"].data_ptr(), out.data_ptr(), 3, int(t["q"].shape[0]), 150, 8, 2, 128, 4,
+        int(t["block_table"].shape[1]), int(t["k_cache"].shape[0]), _ext.i64_array(t["q"].stride()[:2]),
+        _ext.i64_array(t["k_cache"].stride()[:3]), _ext.i64_array(t["v_cache"].stride()[:3]),
+        float(case["scale"]), _ext.UKV_DTYPE_BF16, 16, 16, *st.layer_view(0), torch.cuda.current_stream().cuda_stream)
+    assert code == _ext.UKV_OK
+    torch.cuda.synchronize()
+    check(out.float().cpu().numpy(), expected(case, n_rep=4), "attention output with statistics")
+    rows = st.data[:, 0].cpu().numpy()  # [seq, H_q, obs, (value, flag)]
+    assert np.isfinite(rows[0, ..., 0]).all() and (rows[0, ..., 1] == 0).all()  # 450 keys, middle [16, 434)
+    assert (rows[1] == -7.0).all()                                               # an empty chunk
+    assert (rows[2, :, :11] == -7.0).all()                                       # 5 queries: rows 11 .. 15
+    assert (rows[2, :, 11:, 1] == 1.0).all()                                     # 15 keys, all in the sink
+
+
+@pytest.mark.gpu
 def test_config4_full_size_sampled(cuda):
     """4 sequences x (16384-token prefix + 2048-token chunk), H_q=32, H_kv=8, D=128, bf16."""
     import torch

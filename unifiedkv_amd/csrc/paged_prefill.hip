@@ -698,13 +698,13 @@ __global__ void __launch_bounds__(256) obs_rows_finish_kernel(const PrefillArgs 
   const int i = col / a.n_rep, h = g * a.n_rep + col % a.n_rep;
   const int qi = C - a.obs + i;
   const bool live = col < cols && h < a.Hq && qi >= 0 && C <= a.max_chunk;
+  if (!__any(live)) return;  // (wave-uniform: a chunk shorter than the window, or too long)
   float2* slot = a.obs_stats + (int64_t)b * a.stats_seq_stride + (int64_t)h * a.obs + i;
   const float2 ml = live ? *slot : make_float2(0.f, 0.f);
   const bool ok = live && __builtin_isfinite(ml.x) && ml.y > 0.f && __builtin_isfinite(ml.y);
   const float m = ok ? ml.x : 0.f;
   // B operand: dims 32s + 8kg .. 32s + 8kg + 7 of column i16's query row
-  const uint16_t* qp =
-      a.q + (int64_t)(q_begin + (live ? qi : 0)) * a.q_st + (int64_t)(live ? h : 0) * a.q_sh + 8 * kg;
+  const uint16_t* qp = a.q + (live ? (int64_t)(q_begin + qi) * a.q_st + (int64_t)h * a.q_sh : 0) + 8 * kg;
   u32x4 qv[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) qv[s] = live ? ld16(qp + 32 * s) : u32x4{0u, 0u, 0u, 0u};
