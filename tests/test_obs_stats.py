@@ -20,7 +20,10 @@ Checked here:
   holds most of the weight) and rows that are flagged or non-finite in the given statistics: those items are recomputed by the
   first pass and then equal the two-pass scores bit for bit;
 * the host-side refusals (chunk shorter than the window, a layer not written, another
-  length or softmax scale).
+  length or softmax scale);
+* seeded random shapes through the whole path (dtype, n_rep 1-8, sink, windows of 16-128 queries
+  including one not a multiple of 16, each sequence's own chunk split, sequences too short to
+  score), with the checks above.
 """
 import math
 
@@ -288,6 +291,64 @@ def test_scores_from_prefill_rows_match_two_pass_and_oracle(cuda, dtype):
             got = one[b * layers + layer]
             err = np.abs(got - want)
             assert np.all(err <= 1e-4 * np.abs(want).max() + 1e-3 * np.abs(want)), (b, layer, err.max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_through_the_statistics_path(cuda, seed):
+    """Seeded random shapes: dtype, head layout (n_rep 1-8), sink, window (including one that
+    is not a multiple of 16), batch and each sequence's own chunk split (empty earlier chunks,
+    a final chunk from exactly the window up to the whole sequence). The final chunk's outputs
+    equal the plain prefill's, kept rows match the fp64 normalisers, and the scores from the
+    rows match the two-pass scores and the fp64 oracle."""
+    rng = np.random.default_rng(90000 + seed)
+    dtype = ("bf16", "fp16")[int(rng.integers(2))]
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    n_rep = int(rng.choice([1, 2, 4, 8]))
+    obs = int(rng.choice([16, 24, 32, 48, 64, 128]))
+    sink = int(rng.choice([0, 4, 16, 64]))
+    B = int(rng.integers(1, 4))
+    total = int(rng.integers(sink + obs + 1, 2600))  # at least one middle key
+    n_chunks = int(rng.integers(1, 4))
+    per_seq = []
+    for _ in range(B):
+        # n_chunks - 1 earlier chunks (some possibly empty) split what the final chunk leaves
+        final = int(rng.integers(obs, total + 1)) if n_chunks > 1 else total
+        cuts = np.sort(rng.integers(0, total - final + 1, size=max(0, n_chunks - 2)))
+        parts = np.diff(np.concatenate([[0], cuts, [total - final]])).tolist() if n_chunks > 1 else []
+        per_seq.append(parts + [final])
+    chunks = [[per_seq[b][i] for b in range(B)] for i in range(n_chunks)]
+    chunks = [c for c in chunks[:-1] if sum(c) > 0] + [chunks[-1]]
+    layers = 2
+    r = _prefill(cuda, dtype, chunks, Hq=Hkv * n_rep, Hkv=Hkv, layers=layers, sink=sink, obs=obs, seed=seed)
+    what = f"seed {seed}: {dtype} Hkv {Hkv} n_rep {n_rep} sink {sink} obs {obs} chunks {chunks}"
+    data = r["st"].data.cpu().numpy()
+    for layer in range(layers):
+        out, plain = r["outs"][layer]
+        ok, err, _ = oracle.allclose_report(out, plain, 2e-3, 1e-2)
+        assert ok, f"{what}: layer {layer} output differs from the plain prefill by {err:.3e}"
+        for b in range(B):
+            want = so.obs_row_stats(_f(r["dense"][layer][b], dtype), _f(r["q_obs"][b, layer], dtype), sink_len=sink,
+                                    obs_len=obs, n_rep=n_rep, scale=r["scale"])
+            got, flags = data[b, layer, :, :, 0], data[b, layer, :, :, 1]
+            # (a sequence shorter than sink + window + one block has no middle blocks to score)
+            if want.size and np.any(flags == 0):
+                err = np.abs(got - want)[flags == 0].max()
+                assert err <= LSE_TOL, f"{what}: layer {layer} seq {b} normaliser off by {err:.3e}"
+    r["q_dev"] = _dev(r["q_obs"], dtype)
+    one = _scores(r, sink=sink, obs=obs, stats=True).cpu().numpy()
+    two = _scores(r, sink=sink, obs=obs, stats=False).cpu().numpy()
+    if total < sink + obs + 16:
+        assert one.shape == (B * layers, 0) and two.shape == (B * layers, 0), what
+    np.testing.assert_allclose(one, two, rtol=2.0 ** -9, atol=1e-7, err_msg=what)
+    for b in range(B):
+        for layer in range(layers):
+            want = so.score_layer_blocks(_f(r["dense"][layer][b], dtype), _f(r["q_obs"][b, layer], dtype),
+                                         sink_len=sink, obs_len=obs, n_rep=n_rep)
+            assert want.shape == one[b * layers + layer].shape, what
+            if want.size:
+                err = np.abs(one[b * layers + layer] - want)
+                assert np.all(err <= 1e-4 * np.abs(want).max() + 1e-3 * np.abs(want)), (what, b, layer, err.max())
 
 
 def _statistics_case(cuda):
