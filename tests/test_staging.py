@@ -100,3 +100,27 @@ def test_per_layer_page_lists_round_trip(cuda):
     for l in range(3):
         assert torch.equal(pool.k_cache[l, dst[l]], k0[l])
         assert torch.equal(pool.v_cache[l, dst[l]], v0[l])
+
+
+def test_offload_keeps_callers_device_ids_alive(cuda):
+    """A caller's int32 device id tensor, dropped right after offload() returns, is not handed to
+    the compute stream's next allocation while the side stream's copies still read it: the pages
+    that reach the host are the ones asked for, not those of whatever reuses the freed block."""
+    from unifiedkv_amd.staging import PageStager
+
+    pool = _pool(cuda, N=450, seed=2)
+    rng = np.random.default_rng(7)
+    busy = rng.permutation(450)[:400].tolist()
+    sel = rng.permutation(np.arange(1, 450))[:64].tolist()
+    k0 = pool.k_cache[:, sel].clone()
+    st = PageStager(pool, chunk_pages=8)
+    for _ in range(3):
+        st.offload(busy)  # queues many small copies on the side stream ahead of the next offload
+        ids = torch.tensor(sel, dtype=torch.int32, device=cuda)
+        host = st.offload(ids)
+        del ids
+        junk = torch.empty(len(sel), dtype=torch.int32, device=cuda)  # the allocator's next block of that size
+        junk.fill_(0)  # page 0 (never selected) on the compute stream
+        host.event.synchronize()
+        got = torch.cat([c for c in host.k_chunks], dim=1).to(cuda)
+        assert torch.equal(got, k0)

@@ -83,6 +83,10 @@ class PageStager:
         self.stream.wait_stream(cur)
         with torch.cuda.stream(self.stream):
             ids = self._ids(page_ids)
+            # A caller's int32 device tensor comes back as itself: mark its use on this stream, so
+            # that the caching allocator does not hand its memory to the compute stream while the
+            # copies below still read it.
+            ids.record_stream(self.stream)
             for i, c0 in enumerate(range(0, n, self.chunk)):
                 c = min(self.chunk, n - c0)
                 page_ops.page_copy([pool.k_cache, pool.v_cache], [self.stage_k, self.stage_v], ids[..., c0:c0 + c],
