@@ -336,10 +336,14 @@ def test_prologue_many_pages_in_place_lens_and_table_growth(cuda):
     ids = pool2.allocate_blocks(63)
     batch2 = DecodeBatch(pool2, [ids], [63 * 16 - 1])
     assert batch2.block_table.shape[1] == 64
+    versions = []
     for _ in range(18):
         batch2.begin_step()
         batch2.end_step()
+        versions.append(batch2.table_version)
     assert batch2.block_table.shape[1] == 128
+    # one reallocation, at the step whose new page (column 64) lay past the width
+    assert versions[0] == 0 and versions[-1] == 1 and sorted(versions) == versions
     assert len(batch2.page_lists[0]) == 65
     assert batch2.block_table[0, :65].cpu().tolist() == batch2.page_lists[0]
 

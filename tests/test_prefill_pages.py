@@ -155,3 +155,45 @@ def test_prefill_pages_refuses_a_chunk_the_pool_cannot_hold(cuda):
     assert pool.n_free == 1 and [len(x) for x in pp.page_lists] == [3, 2]
     with pytest.raises(RuntimeError, match="prefill_chunk_not_open"):
         pp.end_chunk()
+
+
+@pytest.mark.gpu
+def test_prefill_pages_chunk_tensors_outlive_a_side_stream(cuda):
+    """The chunk's table and lengths, uploaded on the default stream and read by attention on a
+    side stream that is still busy when end_chunk drops them, are not handed to the default
+    stream's next allocations (which are overwritten with zeros at once): the side stream's
+    output equals the same chunk's on one stream, bit for bit."""
+    import torch
+
+    from unifiedkv_amd.pool import PagedKVPool
+    from unifiedkv_amd.prefill import PrefillPages
+
+    rng = np.random.default_rng(5)
+    Hq, Hkv, D = 8, 2, 128
+    cl = [96, 40]
+    total = sum(cl)
+    q, k, v = _bits(rng, (total, Hq, D)), _bits(rng, (total, Hkv, D)), _bits(rng, (total, Hkv, D))
+    outs = []
+    for side in (False, True):
+        pool = PagedKVPool(16, 1, Hkv, D, torch.bfloat16, num_blocks=64, device=cuda)
+        pp = PrefillPages(pool, 2)
+        pp.begin_chunk(cl)
+        qd, kd, vd = _dev(q), _dev(k), _dev(v)
+        if not side:
+            out = pp.attention(0, qd, kd, vd, softmax_scale=D ** -0.5, n_rep=Hq // Hkv)
+            pp.end_chunk()
+        else:
+            s = torch.cuda.Stream(device=cuda)
+            s.wait_stream(torch.cuda.current_stream(cuda))
+            with torch.cuda.stream(s):
+                torch.cuda._sleep(50_000_000)  # the side stream is still busy after end_chunk
+                out = pp.attention(0, qd, kd, vd, softmax_scale=D ** -0.5, n_rep=Hq // Hkv)
+            pp.end_chunk()
+            # allocations of the chunk tensors' sizes on the default stream, zeroed at once (zero
+            # lengths and page 0: a kernel that read them would attend nothing, never out of bounds)
+            junk = [torch.zeros(n, dtype=torch.int32, device=cuda) for n in (12, 5, 12, 5)]
+            s.synchronize()
+            del junk
+        torch.cuda.synchronize()
+        outs.append(out.view(torch.int16).cpu())
+    assert torch.equal(outs[0], outs[1])

@@ -85,6 +85,10 @@ class DecodeBatch:
     ``seq_page_lists[i]`` is sequence i's page list (its ``gpu_block_map``, shared by all
     layers) and ``seq_lens[i]`` its current length. The lists are owned by the batch from
     here on (``page_lists`` returns them).
+
+    Streams: the device table and lengths are written on the stream current at construction
+    and at each ``begin_step`` and read on the stream current at each layer call; a caller that
+    runs the calls of one batch on several streams orders them itself (``wait_stream``).
     """
 
     def __init__(self, pool: PagedKVPool, seq_page_lists: Sequence[Sequence[int]], seq_lens: Sequence[int], *,
@@ -131,6 +135,7 @@ class DecodeBatch:
         self._lens_dev = [lens, torch.empty_like(lens)]  # [old lengths, attention lengths] of a step
         self._cur = 0
         self._open = False
+        self._table_version = 0
 
     # ------------------------------------------------------------------ state
     @property
@@ -154,8 +159,16 @@ class DecodeBatch:
     def step_parity(self) -> int:
         """0 or 1: which of the two device length buffers holds the lengths before this step. The
         per-layer calls of an open step read the table, those lengths and the other buffer's; a
-        HIP graph captured from them replays correctly at steps of the same parity."""
+        HIP graph captured from them replays correctly at steps of the same parity while
+        ``table_version`` is unchanged."""
         return self._cur
+
+    @property
+    def table_version(self) -> int:
+        """Counts the reallocations of the device table (a step whose new page lies past its
+        width; ``capacity_blocks`` sizes it ahead). Graphs captured from the per-layer calls read
+        the table they were captured with and must be captured again when this changes."""
+        return self._table_version
 
     @property
     def seq_lens(self) -> List[int]:
@@ -243,6 +256,7 @@ class DecodeBatch:
         table = torch.zeros((self.batch, new_w), dtype=torch.int32, device=self.device)
         table[:, :width].copy_(self._table)
         self._table = table
+        self._table_version += 1
 
     def _launch(self, triples: List[Tuple[int, int, int]], lens: bool) -> None:
         if triples:

@@ -15,6 +15,7 @@ from typing import Optional
 import torch
 
 from . import _ext
+from .page16_native import _current_stream
 from .snapkv import ObsStats
 
 _DTYPE_CODES = {torch.float16: _ext.UKV_DTYPE_F16, torch.bfloat16: _ext.UKV_DTYPE_BF16}
@@ -184,6 +185,12 @@ class PrefillPages:
 
     ``page_lists`` / ``seq_lens`` are what ``DecodeBatch``, ``snapkv.score_blocks`` and
     ``compaction.compact`` take next; no dense copy of the prefill KV is ever made.
+
+    Streams: the chunk's table and lengths are uploaded on the stream current at ``begin_chunk``
+    and read on the stream current at each later call; a caller that moves to another stream
+    orders it after the upload itself (``wait_stream``), as for any tensor handed across
+    streams. Each other stream a chunk's tensors are read on is recorded with the caching
+    allocator, so ``end_chunk`` never frees them under that stream's pending kernels.
     """
 
     def __init__(self, pool, num_seqs: Optional[int] = None, *, page_lists=None, seq_lens=None):
@@ -243,14 +250,22 @@ class PrefillPages:
             cu.append(cu[-1] + c)
         kv = [L + c for L, c in zip(self._lens, chunk_lens)]
         small = torch.tensor(cu + kv, dtype=torch.int32).pin_memory().to(self.dev, non_blocking=True)
-        self._chunk = dict(bt=host.pin_memory().to(self.dev, non_blocking=True), cu=small[:len(cu)],
-                           kv=small[len(cu):], max_chunk=max(chunk_lens), lens=chunk_lens, total=cu[-1])
+        self._chunk = dict(bt=host.pin_memory().to(self.dev, non_blocking=True), small=small, cu=small[:len(cu)],
+                           kv=small[len(cu):], max_chunk=max(chunk_lens), lens=chunk_lens, total=cu[-1],
+                           streams={_current_stream(self.dev)})
         return self._chunk["bt"], self._chunk["cu"], self._chunk["kv"], self._chunk["max_chunk"]
 
     def _open(self):
         if self._chunk is None:
             raise RuntimeError("prefill_chunk_not_open")
-        return self._chunk
+        c = self._chunk
+        cur = _current_stream(self.dev)
+        if cur not in c["streams"]:  # read on a stream other than the upload's: keep them alive for it
+            s = torch.cuda.current_stream(self.dev)
+            c["bt"].record_stream(s)
+            c["small"].record_stream(s)
+            c["streams"].add(cur)
+        return c
 
     def write(self, layer_id: int, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """The layer's chunk K/V, packed [total_q, H_kv, D] in batch order, into their pages."""
