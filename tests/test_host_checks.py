@@ -83,6 +83,10 @@ def test_score_blocks_rejects_short_or_foreign_tables():
     q, k, bt = _score_args()
     with pytest.raises(RuntimeError, match="bad_score_device"):  # meta is not a GPU
         snapkv.score_blocks(q, k, bt, seq_len=512, sink_len=16, obs_len=16, n_rep=4)
+    # a pool view whose key rows are not contiguous (the C entry point has no stride for D)
+    k_t = torch.empty((2, 64, 16, 64, 2), dtype=torch.float16, device=META).transpose(3, 4)
+    with pytest.raises(RuntimeError, match="k_pool_stride"):
+        snapkv.score_blocks(q, k_t, bt, seq_len=512, sink_len=16, obs_len=16, n_rep=4)
 
 
 class _FakePool:

@@ -258,14 +258,17 @@ class PrefillPages:
     def _open(self):
         if self._chunk is None:
             raise RuntimeError("prefill_chunk_not_open")
-        c = self._chunk
+        return self._chunk
+
+    def _read_here(self, c) -> None:
+        """Before a launch that reads the chunk's tensors: on a stream other than the upload's,
+        record them there, so that the caching allocator keeps them for its pending kernels."""
         cur = _current_stream(self.dev)
-        if cur not in c["streams"]:  # read on a stream other than the upload's: keep them alive for it
+        if cur not in c["streams"]:
             s = torch.cuda.current_stream(self.dev)
             c["bt"].record_stream(s)
             c["small"].record_stream(s)
             c["streams"].add(cur)
-        return c
 
     def write(self, layer_id: int, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """The layer's chunk K/V, packed [total_q, H_kv, D] in batch order, into their pages."""
@@ -276,6 +279,7 @@ class PrefillPages:
             raise IndexError(f"layer {layer_id} is outside the pool's {pool.num_layers} layers")
         if c["total"] == 0:
             return
+        self._read_here(c)
         if (k_new.dtype != pool.dtype or v_new.dtype != pool.dtype or k_new.device != self.dev
                 or tuple(k_new.shape) != (c["total"], pool.num_kv_heads, pool.head_dim)
                 or k_new.stride() != v_new.stride() or k_new.stride(-1) != 1):
@@ -306,6 +310,7 @@ class PrefillPages:
         if c["total"] == 0 and obs_stats is None:
             return torch.empty_like(q)
         self.write(layer_id, k_new, v_new)
+        self._read_here(c)
         host_lens = None
         if obs_stats is not None:
             host_lens = (c["lens"], [L + n for L, n in zip(self._lens, c["lens"])])

@@ -152,6 +152,8 @@ def score_blocks(q_obs: torch.Tensor, k_pool: torch.Tensor, block_table: torch.T
         raise RuntimeError("selected_writeback_bad_score_shape")
     if int(k_pool.shape[2]) != 16:
         raise RuntimeError("selected_writeback_bad_score_shape")
+    if int(k_pool.stride(4)) != 1:  # the kernel reads 16-byte runs of a key row; the ABI carries no dim stride
+        raise RuntimeError("selected_writeback_bad_score_shape:k_pool_stride")
     n = block_count(seq_len, sink_len, obs_len, block_size)
     out = torch.empty((seqs * layers, n), dtype=torch.float32, device=q_obs.device)
     if n == 0:
