@@ -116,3 +116,27 @@ def test_prefill_write_rejects_out_of_range_layers():
 def test_decode_batch_rejects_pages_shared_between_sequences():
     with pytest.raises(ValueError, match="more than one sequence"):
         DecodeBatch(_FakePool(), [[1, 2], [3, 2]], [20, 20])
+
+
+def test_token_io_and_page_copy_refuse_mismatched_or_host_tensors():
+    pool = _pool_layer(H=2, D=64)
+    with pytest.raises(ValueError, match="does not hold the pool's 2 heads x 64 dims"):
+        page_ops.scatter_tokens(pool, [0, 1], torch.empty((1, 20, 64), dtype=torch.float16, device=META))
+    with pytest.raises(ValueError, match="does not hold"):
+        page_ops.scatter_tokens(pool, [0, 1], torch.empty((2, 20, 32), dtype=torch.float16, device=META))
+    with pytest.raises(ValueError, match="one dtype"):
+        page_ops.scatter_tokens(pool, [0, 1], torch.empty((2, 20, 64), dtype=torch.bfloat16, device=META))
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.scatter_tokens(pool, [0, 1], torch.empty((2, 20, 64), dtype=torch.float16, device=META))
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.gather_tokens(_pool_layer(dev="cpu"), [0], 4)
+    stacked = torch.empty((2, 8, 16, 2, 64), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        page_ops.page_copy([stacked], [stacked], [0], [1])
+
+
+def test_select_blocks_refuses_host_scores():
+    from unifiedkv_amd import compaction
+
+    with pytest.raises(RuntimeError, match="must be on a GPU"):
+        compaction.select_blocks(torch.rand((2, 10)), 3)

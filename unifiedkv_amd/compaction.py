@@ -73,6 +73,8 @@ def select_blocks(scores: torch.Tensor, k: int, n_valid: Optional[torch.Tensor] 
         scores = scores.contiguous()
     rows, n = int(scores.shape[0]), int(scores.shape[1])
     dev = scores.device
+    if dev.type != "cuda":
+        raise RuntimeError(f"select_blocks: scores must be on a GPU, got {dev}")
     out = torch.empty((rows, max(int(k), 0)), dtype=torch.int32, device=dev)
     if rows == 0 or k <= 0:
         return out

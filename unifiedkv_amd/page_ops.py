@@ -29,6 +29,15 @@ def _check_rows(t: torch.Tensor, what: str):
         raise ValueError(f"{what}: last dimension must be contiguous")
 
 
+def _check_gpu(dev: torch.device, others, fn: str):
+    """Every tensor the kernel dereferences on the one GPU ``dev``, checked before any launch."""
+    if dev.type != "cuda":
+        raise RuntimeError(f"{fn}: tensors must be on a GPU, got {dev}")
+    for t, w in others:
+        if t.device != dev:
+            raise RuntimeError(f"{fn}: {w} is on {t.device}, the pool on {dev}")
+
+
 def scatter_tokens(pool_layer: torch.Tensor, page_ids, dense: torch.Tensor, n_tokens: Optional[int] = None) -> None:
     """pool_layer[page_ids[t // bs], t % bs, h, :] = dense[h, t, :] for t < n_tokens (bs = pool_layer.shape[1]).
 
@@ -37,9 +46,15 @@ def scatter_tokens(pool_layer: torch.Tensor, page_ids, dense: torch.Tensor, n_to
     _check_rows(pool_layer, "pool_layer")
     _check_rows(dense, "dense")
     dev = pool_layer.device
+    if pool_layer.dim() != 4 or dense.dim() != 3 or dense.dtype != pool_layer.dtype:
+        raise ValueError("scatter_tokens: pool_layer [N, bs, H, D] and dense [H, T, D] of one dtype required")
+    if int(dense.shape[0]) != int(pool_layer.shape[2]) or int(dense.shape[2]) != int(pool_layer.shape[3]):
+        raise ValueError(f"scatter_tokens: dense {list(dense.shape)} does not hold the pool's "
+                         f"{int(pool_layer.shape[2])} heads x {int(pool_layer.shape[3])} dims")
+    _check_gpu(dev, [(dense, "dense")], "scatter_tokens")
     ids = _i32(page_ids, dev)
     bs = int(pool_layer.shape[1])
-    T = int(dense.shape[1]) if n_tokens is None else int(n_tokens)
+    T = int(dense.shape[1]) if n_tokens is None else min(int(n_tokens), int(dense.shape[1]))
     T = min(T, bs * int(ids.numel()))
     if T <= 0:
         return
@@ -54,6 +69,9 @@ def gather_tokens(pool_layer: torch.Tensor, page_ids, n_tokens: int) -> torch.Te
     """[H, n, D] with row t = pool_layer[page_ids[t // bs], t % bs], n = min(n_tokens, bs * len(ids))."""
     _check_rows(pool_layer, "pool_layer")
     dev = pool_layer.device
+    if pool_layer.dim() != 4:
+        raise ValueError("gather_tokens: pool_layer [N, bs, H, D] required")
+    _check_gpu(dev, [], "gather_tokens")
     ids = _i32(page_ids, dev)
     bs = int(pool_layer.shape[1])
     H, D = int(pool_layer.shape[2]), int(pool_layer.shape[3])
@@ -79,6 +97,7 @@ def page_copy(src_pools: Sequence[torch.Tensor], dst_pools: Sequence[torch.Tenso
         raise ValueError("page_copy: one or two (src, dst) pool pairs")
     s0, d0 = src_pools[0], dst_pools[0]
     dev = s0.device
+    _check_gpu(dev, [(t, "a pool") for t in list(src_pools[1:]) + list(dst_pools)], "page_copy")
     L = int(s0.shape[0])
     page_elems = int(s0[0, 0].numel())
     for s, d in zip(src_pools, dst_pools):
