@@ -140,3 +140,23 @@ def test_select_blocks_refuses_host_scores():
 
     with pytest.raises(RuntimeError, match="must be on a GPU"):
         compaction.select_blocks(torch.rand((2, 10)), 3)
+
+
+def test_write_chunk_kv_refuses_rows_that_do_not_match_the_pool():
+    from unifiedkv_amd import prefill
+
+    pool = _pool_layer(H=2, D=64)
+    bt = torch.empty((2, 4), dtype=torch.int32, device=META)
+    lens = torch.empty((2,), dtype=torch.int32, device=META)
+    rows = lambda n, h=2, d=64: torch.empty((n, h, d), dtype=torch.float16, device=META)  # noqa: E731
+    with pytest.raises(ValueError, match=r"must be \[total, 2, 64\]"):
+        prefill.write_chunk_kv(pool, pool, rows(10, h=1), rows(10, h=1), bt, [0, 4, 10], lens)
+    with pytest.raises(ValueError, match=r"must be \[total, 2, 64\]"):
+        prefill.write_chunk_kv(pool, pool, rows(10), rows(9), bt, [0, 4, 10], lens)
+    with pytest.raises(RuntimeError, match="paged_prefill_unavailable:device"):  # meta is not a GPU
+        prefill.write_chunk_kv(pool, pool, rows(10), rows(10), bt, [0, 4, 10], lens)
+    cpu_pool = _pool_layer(H=2, D=64, dev="cpu")
+    cpu_rows = torch.empty((8, 2, 64), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="paged_prefill_unavailable:device"):
+        prefill.write_chunk_kv(cpu_pool, cpu_pool, cpu_rows, cpu_rows, torch.zeros((2, 4), dtype=torch.int32),
+                               [0, 4, 8], torch.zeros((2,), dtype=torch.int32))

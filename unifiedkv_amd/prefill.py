@@ -63,13 +63,27 @@ def write_chunk_kv(k_layer: torch.Tensor, v_layer: torch.Tensor, k_new: torch.Te
     for t in (k_layer, v_layer, k_new, v_new):
         if t.dtype != k_layer.dtype or t.stride(-1) != 1:
             raise ValueError("write_chunk_kv: one 16-bit dtype, contiguous last dimension")
+    # Everything the kernel dereferences, checked before the launch: the rows it reads are
+    # k_new[cu[b] + i] for i < C_b, so the chunk rows must hold every head and dim of the pool.
+    if k_layer.dim() != 4 or tuple(v_layer.shape) != tuple(k_layer.shape):
+        raise ValueError("write_chunk_kv: k_layer / v_layer must be equal [N, 16, H_kv, D] tensors")
+    if k_new.dim() != 3 or tuple(k_new.shape[1:]) != tuple(k_layer.shape[2:]) or v_new.shape != k_new.shape:
+        raise ValueError(f"write_chunk_kv: k_new / v_new must be [total, {int(k_layer.shape[2])}, "
+                         f"{int(k_layer.shape[3])}] tensors of one shape")
+    if dev.type != "cuda" or any(t.device != dev for t in (v_layer, k_new, v_new)):
+        raise RuntimeError("paged_prefill_unavailable:device")
+    chunk_lens = _chunk_lens_on_host(cu_seqlens_q)
+    if chunk_lens is not None and sum(chunk_lens) > int(k_new.shape[0]):
+        raise ValueError(f"write_chunk_kv: the chunks hold {sum(chunk_lens)} rows, k_new {int(k_new.shape[0])}")
     if k_new.stride() != v_new.stride():
         k_new, v_new = k_new.contiguous(), v_new.contiguous()
     cu = _i32(cu_seqlens_q, dev)
     lens = _i32(kv_lens, dev)
     bt = _i32(block_table, dev)
     B = int(lens.numel())
-    mc = _max_chunk(cu_seqlens_q, max_chunk)
+    if int(cu.numel()) != B + 1 or bt.dim() != 2 or int(bt.shape[0]) != B:
+        raise RuntimeError("paged_prefill_shape_unsupported:batch")
+    mc = _max_chunk(cu_seqlens_q, max_chunk, chunk_lens)
     code = _ext.load().ukv_kv_write_varlen(
         k_layer.data_ptr(), v_layer.data_ptr(), _ext.i64_array(k_layer.stride()[:3]),
         _ext.i64_array(v_layer.stride()[:3]), k_new.data_ptr(), v_new.data_ptr(), _ext.i64_array(k_new.stride()[:2]),
